@@ -1,0 +1,240 @@
+"""Benchmark: fwd+bwd attention TFLOPS and % of MI355X MFMA peak.
+
+Workload (the north-star configuration): bf16 causal
+GQA, B=2 Hq=32 Hkv=8 D=128 S=4096, synthetic N(0,1) inputs already resident
+in HBM.  One step = forward (O, LSE) + backward (Delta, dQ, dK/dV), exactly
+what npu_flash_attention_forward + npu_flash_attention_backward launch.
+
+FLOP convention: fwd = 4*D*N_pairs*B*Hq over attended (i, j) pairs only,
+bwd = 2.5 * fwd (recomputation not counted).  Peak = 2516.6 TFLOP/s
+(256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU).
+
+Prints ONE JSON line.  Per-kernel times come from HIP events recorded on the
+stream the kernels are launched on (torch's current stream).
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "npu-flex-att_amd"))
+
+PEAK_TFLOPS = 2516.6  # dense bf16/fp16 MFMA
+
+CONFIGS = {
+    # name: (B, Hq, Hkv, Sq, Skv, D, dtype, causal, window, soft_cap, alibi, scale, input_scale)
+    "gqa_llama3_8b": (2, 32, 8, 4096, 4096, 128, "bf16", True, 0, 0.0, False, None, 1.0),
+    "gemma2_d256": (1, 16, 8, 8192, 8192, 256, "bf16", True, 4096, 50.0, False, 1.0 / 16, 2.0),
+    "all_primitives_d64": (1, 28, 4, 16384, 16383, 64, "fp16", True, 2048, 30.0, True, 0.05, 1.0),
+    "mha_d64_s2048": (1, 2, 2, 2048, 2048, 64, "fp16", True, 0, 0.0, False, None, 1.0),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="gqa_llama3_8b", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bounded CPU baseline sample budget")
+    return ap.parse_args()
+
+
+def pairs(sq, skv, causal, window):
+    total = 0
+    for i in range(sq):
+        hi = min(skv - 1, i) if causal else skv - 1
+        lo = max(0, i - window) if window > 0 else 0
+        total += max(0, hi - lo + 1)
+    return total
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(attention over (batch, KV-head) groups shards with no communication; see DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import flexatt_lib as L
+    import npu_flash_attention as nfa
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, Sq, Skv, D, dts, causal, window, cap, alibi, scale, insc = CONFIGS[args.config]
+    dtype = {"bf16": torch.bfloat16, "fp16": torch.float16}[dts]
+    g = torch.Generator().manual_seed(42)
+    q = (torch.randn(B, Hq, Sq, D, generator=g) * insc).to(dtype).to(dev)
+    k = (torch.randn(B, Hkv, Skv, D, generator=g) * insc).to(dtype).to(dev)
+    v = (torch.randn(B, Hkv, Skv, D, generator=g) * insc).to(dtype).to(dev)
+    do = torch.randn(B, Hq, Sq, D, generator=g).to(dtype).to(dev)
+    slopes = None
+    if alibi:
+        slopes = torch.tensor([2.0 ** (-8.0 * (h + 1) / Hq) for h in range(Hq)], dtype=torch.float32, device=dev)
+    kw = dict(causal=causal, sliding_window=window, soft_cap=cap, scale=scale, alibi_slope=slopes)
+
+    npairs = pairs(Sq, Skv, causal, window)
+    fwd_flop = 4.0 * D * npairs * B * Hq
+    bwd_flop = 2.5 * fwd_flop
+
+    def step():
+        o, lse = nfa.npu_flash_attention_forward(q, k, v, return_lse=True, **kw)
+        nfa.npu_flash_attention_backward(q, k, v, o, lse, do, **kw)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # Per-kernel durations through the C ABI, HIP events on the launch stream.
+    lib = L.load()
+    o, lse = nfa.npu_flash_attention_forward(q, k, v, return_lse=True, **kw)
+    delta = torch.empty(B, Hq, Sq, dtype=torch.float32, device=dev)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    p = nfa._problem(q, k, scale if scale is not None else 1.0 / math.sqrt(D), causal, window, cap, slopes)
+    st = torch.cuda.current_stream(dev)
+    sh = st.cuda_stream
+    T = L.tensor
+    calls = {
+        "fwd": lambda: lib.flexatt_fwd(p, T(q), T(k), T(v), T(o), lse.data_ptr(), sh),
+        "delta": lambda: lib.flexatt_bwd_delta(p, T(o), T(do), delta.data_ptr(), sh),
+        "dq": lambda: lib.flexatt_bwd_dq(p, T(q), T(k), T(v), T(do), lse.data_ptr(), delta.data_ptr(), T(dq), sh),
+        "dkdv": lambda: lib.flexatt_bwd_dkdv(p, T(q), T(k), T(v), T(do), lse.data_ptr(), delta.data_ptr(),
+                                             T(dk), T(dv), sh),
+    }
+    reps = max(args.steps, 10)
+    kernel_ms = {}
+    for name, fn in calls.items():
+        for _ in range(3):
+            L.check(fn(), name)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in evs:
+            a.record(st)
+            L.check(fn(), name)
+            b.record(st)
+        torch.cuda.synchronize()
+        kernel_ms[name] = statistics.median(a.elapsed_time(b) for a, b in evs)
+
+    fwd_ms = kernel_ms["fwd"]
+    bwd_ms = kernel_ms["delta"] + kernel_ms["dq"] + kernel_ms["dkdv"]
+    fwd_tf = fwd_flop / fwd_ms / 1e9
+    bwd_tf = bwd_flop / bwd_ms / 1e9
+    total_tf = (fwd_flop + bwd_flop) / ms_step / 1e9
+    # dominant kernel = the longest one; its algorithmic FLOPs per launch:
+    # fwd: 4*D*pairs*B*Hq; dQ: 3 GEMMs of the 5 backward ones (S recompute,
+    # dP, dS K) = 6*D*pairs*B*Hq; dK/dV: 4 GEMMs (S, dP, P^T dO, dS^T Q) = 8*D*...
+    per_kernel_flop = {"fwd": fwd_flop, "dq": 6.0 * D * npairs * B * Hq, "dkdv": 8.0 * D * npairs * B * Hq}
+    dom = max(per_kernel_flop, key=lambda n: kernel_ms[n])
+    achieved = per_kernel_flop[dom] / kernel_ms[dom] / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(q, k, v, do, kw, slopes, args.cpu_seconds, Hq // Hkv, causal, window, D, Sq, Skv)
+
+    out = {
+        "metric": "fwd+bwd attention TFLOPS & % MFMA peak, bf16 causal GQA D=128 S=4096",
+        "value": round(total_tf, 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dts,
+        "data": "synthetic N(0,1), seed 42, resident in HBM",
+        "config": {
+            "workload": f"{args.config}: {dts} B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} Skv={Skv} D={D} causal={causal} "
+                        f"window={window} soft_cap={cap} alibi={alibi} scale={scale}; step = fwd + bwd",
+            "batch": B, "heads_q": Hq, "heads_kv": Hkv, "seqlen_q": Sq, "seqlen_kv": Skv, "head_dim": D,
+            "parallelism": "single GPU",
+        },
+        "fwd_ms": round(fwd_ms, 4),
+        "bwd_ms": round(bwd_ms, 4),
+        "kernel_ms": {k_: round(v_, 4) for k_, v_ in kernel_ms.items()},
+        "fwd_tflops": round(fwd_tf, 1),
+        "bwd_tflops": round(bwd_tf, 1),
+        "fwd_frac_peak": round(fwd_tf / PEAK_TFLOPS, 4),
+        "bwd_frac_peak": round(bwd_tf / PEAK_TFLOPS, 4),
+        "frac_peak": round(total_tf / PEAK_TFLOPS, 4),
+        "roofline": {
+            "kernel": dom,
+            "bound": "mfma",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_TFLOPS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(q, k, v, do, kw, slopes, budget_s, G, causal, window, D, Sq, Skv):
+    """The fp32 eager math path (the oracle) on the host cores, over as many
+    (batch, KV-head) groups of the same workload as fit the time budget."""
+    import torch
+
+    from oracle import attention_oracle as orc
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    qc, kc, vc, dc = (t.float().cpu() for t in (q, k, v, do))
+    sl = None if slopes is None else slopes.cpu()
+    B, Hkv = kc.shape[0], kc.shape[1]
+    done = 0
+    t0 = time.perf_counter()
+    for b in range(B):
+        for h in range(Hkv):
+            hs = slice(h * G, (h + 1) * G)
+            o, lse = orc.forward(qc[b:b + 1, hs], kc[b:b + 1, h:h + 1], vc[b:b + 1, h:h + 1], causal, window,
+                                 None if sl is None else sl[hs], kw["scale"], kw["soft_cap"], torch.float32)
+            orc.backward(qc[b:b + 1, hs], kc[b:b + 1, h:h + 1], vc[b:b + 1, h:h + 1], dc[b:b + 1, hs], causal,
+                         window, None if sl is None else sl[hs], kw["scale"], kw["soft_cap"], torch.float32, o=o)
+            done += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+        else:
+            continue
+        break
+    secs = time.perf_counter() - t0
+    flop = 3.5 * 4.0 * D * pairs(Sq, Skv, causal, window) * G * done
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(flop / secs / 1e12, 4),
+        "unit": "TFLOPS",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{done} of {B * Hkv} (batch, KV-head) groups ({done * G} query heads), fwd+bwd fp32 eager "
+                  f"oracle, {secs:.1f} s on {cpu_model or 'host CPU'}",
+    }
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,120 @@
+/*
+ * flexatt.h — C ABI of the MI355X (gfx950) flash-attention library
+ * (libflexatt.so).
+ *
+ * The reference (dropletzhu/npu-flex-att) has no C ABI: its host wrappers in
+ * npu_flash_attention.py launch Triton kernels directly.  Each entry point
+ * below replaces one such launch (or one torch op of the wrapper) and is what
+ * a foreign-function binding of that wrapper calls; the Python host layer of
+ * this repository binds them with ctypes.
+ *
+ * Conventions
+ *  - Tensors are 4-D [B, H, S, D] views: a device pointer plus element
+ *    strides.  The innermost stride must be 1 and every row must start on a
+ *    16-byte boundary (data pointer and the b/h/s strides times the element
+ *    size are multiples of 16 bytes).  Batch and head strides may be 0
+ *    (broadcast).
+ *  - q, o, dout and dq have shape [B, Hq, Sq, D]; k, v, dk and dv have shape
+ *    [B, Hkv, Skv, D]; Hq is a multiple of Hkv and query head h reads KV head
+ *    h / (Hq / Hkv).
+ *  - lse and delta are contiguous fp32 [B, Hq, Sq]; lse is the natural-log
+ *    log-sum-exp of the masked, scaled (and soft-capped, ALiBi-biased) scores.
+ *  - All work is enqueued on `stream` (a hipStream_t; NULL = the null
+ *    stream) and is asynchronous.  Nothing is allocated or freed: the caller
+ *    owns every buffer.  Results are bitwise deterministic.
+ *  - Return value: FLEXATT_OK, a negative FLEXATT_E* code for a rejected
+ *    argument (nothing is launched), or a positive hipError_t from a launch.
+ */
+#ifndef FLEXATT_H_
+#define FLEXATT_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of q/k/v/o/dout/dq/dk/dv. */
+enum flexatt_dtype { FLEXATT_F32 = 0, FLEXATT_F16 = 1, FLEXATT_BF16 = 2 };
+
+/* Status codes (negative: argument rejected before any launch). */
+enum flexatt_status {
+  FLEXATT_OK = 0,
+  FLEXATT_EINVAL = -1,     /* null pointer, non-positive size, bad flag */
+  FLEXATT_EDTYPE = -2,     /* unknown dtype */
+  FLEXATT_EHEADDIM = -3,   /* head_dim not in {32, 64, 128, 256} */
+  FLEXATT_ESHAPE = -4,     /* heads_q % heads_kv != 0, or sizes overflow */
+  FLEXATT_ELAYOUT = -5     /* innermost stride != 1 or a row not 16-byte aligned */
+};
+
+/* One [B, H, S, D] tensor: device pointer and element strides. */
+typedef struct flexatt_tensor {
+  void* data;
+  int64_t stride_b, stride_h, stride_s, stride_d;
+} flexatt_tensor;
+
+/* The attention problem: sizes and the mask primitives.
+ * npu_flash_attention.py:606-616 (forward signature) and :659-668 (backward)
+ * carry the same fields as Python arguments; block_m / block_n are tiling
+ * hints there and have no counterpart here. */
+typedef struct flexatt_problem {
+  int32_t dtype;          /* enum flexatt_dtype */
+  int32_t batch;          /* B */
+  int32_t heads_q;        /* Hq */
+  int32_t heads_kv;       /* Hkv */
+  int32_t seqlen_q;       /* Sq */
+  int32_t seqlen_kv;      /* Skv (any value >= 1; no tile-multiple requirement) */
+  int32_t head_dim;       /* D in {32, 64, 128, 256} */
+  float scale;            /* softmax scale (the caller applies the 1/sqrt(D) default) */
+  int32_t causal;         /* 1: keep j <= i (top-left aligned) */
+  int32_t sliding_window; /* W > 0: keep i - j <= W; 0: off */
+  float soft_cap;         /* c > 0: x -> c * tanh(x / c); 0: off */
+  const float* alibi_slopes; /* device fp32 [Hq]: x += slope[h] * (i - j); NULL: off */
+} flexatt_problem;
+
+/* Forward: o = softmax(mask(score(q k^T))) v and lse.
+ * Replaces the flash_attn_fwd_kernel launch of npu_flash_attention_forward,
+ * npu_flash_attention.py:634-652. */
+int flexatt_fwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                const flexatt_tensor* v, const flexatt_tensor* o, float* lse, void* stream);
+
+/* Backward pre-pass: delta[b,h,i] = sum_d o * dout in fp32.
+ * Replaces the torch op at npu_flash_attention.py:681-685. */
+int flexatt_bwd_delta(const flexatt_problem* p, const flexatt_tensor* o, const flexatt_tensor* dout,
+                      float* delta, void* stream);
+
+/* Backward dQ (needs lse and delta).
+ * Replaces the flash_attn_bwd_dq_kernel launch, npu_flash_attention.py:695-712. */
+int flexatt_bwd_dq(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                   const flexatt_tensor* v, const flexatt_tensor* dout, const float* lse,
+                   const float* delta, const flexatt_tensor* dq, void* stream);
+
+/* Backward dK/dV with the GQA group sum folded in: dk/dv are [B, Hkv, Skv, D].
+ * Replaces the flash_attn_bwd_dkdv_kernel launch plus the group sum,
+ * npu_flash_attention.py:714-737. */
+int flexatt_bwd_dkdv(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                     const flexatt_tensor* v, const flexatt_tensor* dout, const float* lse,
+                     const float* delta, const flexatt_tensor* dk, const flexatt_tensor* dv,
+                     void* stream);
+
+/* Whole backward: delta (into the caller's fp32 [B,Hq,Sq] `delta` buffer),
+ * then dQ, then dK/dV.  Replaces the kernel launches and torch ops of
+ * npu_flash_attention_backward, npu_flash_attention.py:659-739. */
+int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                const flexatt_tensor* v, const flexatt_tensor* o, const flexatt_tensor* dout,
+                const float* lse, float* delta, const flexatt_tensor* dq, const flexatt_tensor* dk,
+                const flexatt_tensor* dv, void* stream);
+
+/* Human-readable text for a status code (static storage). */
+const char* flexatt_status_string(int status);
+
+/* ABI version of this header (bumped on any signature change). */
+int flexatt_abi_version(void);
+
+#define FLEXATT_ABI_VERSION 1
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLEXATT_H_ */

@@ -1,0 +1,437 @@
+// Flash-attention backward for fp16/bf16 on gfx950 MFMA: the dQ kernel and
+// the dK/dV kernel.  Delta = rowsum(O * dO) comes from the pre-kernel in
+// delta.hip.
+//
+// Semantics: npu_flash_attention.py:298-402 (flash_attn_bwd_dq_kernel) and
+// :407-560 (flash_attn_bwd_dkdv_kernel): P is recomputed from the forward LSE,
+// dP = dO V^T, dS = P (dP - Delta) scale (1 - tanh^2), dQ = dS K,
+// dK = dS^T Q, dV = P^T dO; P and dS are rounded to the input dtype before
+// their MFMAs, as the reference does before tl.dot.  Two deliberate
+// differences: the ALiBi bias is part of the recomputed P (the reference's
+// backward kernels take no ALiBi argument), and dK/dV are accumulated over the
+// G query heads of a group in fp32 inside the kernel (the reference writes
+// per-query-head partials and sums them in the input dtype,
+// npu_flash_attention.py:734-737).
+//
+// dQ: one workgroup = 4 waves = 128 query rows of one (b, hq); per 64-row KV
+//     tile each wave forms S^T = K Q^T and dP^T = V dO^T (lane = query row),
+//     then dQ^T += K^T dS^T with K^T read by the LDS transpose read.
+// dK/dV: one workgroup = 4 waves = 128 KV rows of one (b, hkv); K and V rows
+//     live in registers; the workgroup walks the G query heads of the group
+//     and their 64-row query tiles, forming S = Q K^T and dP = dO V^T
+//     (lane = KV row), then dV^T += dO^T P and dK^T += Q^T dS with dO^T and
+//     Q^T read by the LDS transpose read.
+// Both kernels are deterministic: every output element is owned by one lane
+// and accumulated in a fixed order.
+#include "flexatt_device.h"
+#include "flexatt_kernels.h"
+
+#ifndef FLEXATT_D
+#error "FLEXATT_D (head dim) must be defined"
+#endif
+
+namespace flexatt {
+
+template <int D>
+struct BwdCfg {
+  static constexpr int NW = 4;
+  static constexpr int KC = D / 16;
+  static constexpr int DB = D / 32;
+  static constexpr int P = D + 8;
+  static constexpr int CPR = D / 8;
+  // dQ kernel
+  static constexpr int BM = 32 * NW;
+  static constexpr int BN = 64;
+  static constexpr int CPT = BN * CPR / (NW * 64);
+  // dK/dV kernel
+  static constexpr int BNK = 32 * NW;
+  static constexpr int BMQ = 64;
+  static constexpr int CPTQ = BMQ * CPR / (NW * 64);
+  static constexpr bool PREFETCH = D <= 128;
+};
+
+// ---------------------------------------------------------------- dQ kernel --
+template <class T, int D, bool SOFTCAP, bool ALIBI>
+__global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(BwdArgs a) {
+  using C = BwdCfg<D>;
+  using M = Mfma<T>;
+  using V8 = typename M::v8;
+  __shared__ __attribute__((aligned(16))) T sK[C::BN * C::P];
+  __shared__ __attribute__((aligned(16))) T sV[C::BN * C::P];
+
+  const Shape& p = a.p;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = a.ntiles - 1 - (w % a.ntiles);
+  const int bh = w / a.ntiles;
+  const int hq = bh % p.Hq, b = bh / p.Hq;
+  const int hk = hq / p.G;
+  const int m0 = qt * C::BM;
+  const int mw = m0 + wave * 32;
+  const int my_m = mw + l32;
+
+  const T* qp = (const T*)a.q.data + b * a.q.sb + hq * a.q.sh;
+  const T* dop = (const T*)a.dout.data + b * a.dout.sb + hq * a.dout.sh;
+  const T* kp = (const T*)a.k.data + b * a.k.sb + hk * a.k.sh;
+  const T* vp = (const T*)a.v.data + b * a.v.sb + hk * a.v.sh;
+
+  V8 qf[C::KC], dof[C::KC];
+  {
+    const int r = min(my_m, p.Sq - 1);
+    const T* sq = qp + (int64_t)r * a.q.ss + 8 * h;
+    const T* sd = dop + (int64_t)r * a.dout.ss + 8 * h;
+#pragma unroll
+    for (int kc = 0; kc < C::KC; ++kc) {
+      i32x4 x = ld_global16(sq + 16 * kc), y = ld_global16(sd + 16 * kc);
+      if (my_m >= p.Sq) { x = i32x4{0, 0, 0, 0}; y = i32x4{0, 0, 0, 0}; }
+      qf[kc] = as_v8<V8>(x);
+      dof[kc] = as_v8<V8>(y);
+    }
+  }
+  // log2-domain LSE; +inf makes P exactly 0 for fully-masked or padding rows.
+  float lse2 = kPosInf, dl = 0.f;
+  if (my_m < p.Sq) {
+    const int64_t ri = (int64_t)(b * p.Hq + hq) * p.Sq + my_m;
+    const float l = a.lse[ri];
+    lse2 = (l == kNegInf) ? kPosInf : l * kLog2e;
+    dl = a.delta[ri];
+  }
+
+  int kv_lo = 0, kv_hi = p.Skv;
+  if (p.causal) kv_hi = min(kv_hi, m0 + C::BM);
+  if (p.window > 0) kv_lo = max(0, m0 - p.window);
+  const int t_lo = kv_lo / C::BN;
+  const int t_hi = (kv_hi + C::BN - 1) / C::BN;
+
+  i32x4 rk[C::CPT], rv[C::CPT];
+  auto gload = [&](int t) {
+    const int n0 = t * C::BN;
+#pragma unroll
+    for (int e = 0; e < C::CPT; ++e) {
+      const int c = tid + e * C::NW * 64;
+      const int row = c / C::CPR, col = (c % C::CPR) * 8;
+      const int n = n0 + row;
+      const int nc = min(n, p.Skv - 1);
+      i32x4 xk = ld_global16(kp + (int64_t)nc * a.k.ss + col);
+      i32x4 xv = ld_global16(vp + (int64_t)nc * a.v.ss + col);
+      if (n >= p.Skv) { xk = i32x4{0, 0, 0, 0}; xv = i32x4{0, 0, 0, 0}; }
+      rk[e] = xk;
+      rv[e] = xv;
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int e = 0; e < C::CPT; ++e) {
+      const int c = tid + e * C::NW * 64;
+      const int row = c / C::CPR, col = (c % C::CPR) * 8;
+      *(i32x4*)&sK[row * C::P + col] = rk[e];
+      *(i32x4*)&sV[row * C::P + col] = rv[e];
+    }
+  };
+
+  f32x16 acc[C::DB];
+#pragma unroll
+  for (int db = 0; db < C::DB; ++db) acc[db] = f32x16{};
+  const float slope_log2 = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
+
+  if (C::PREFETCH && t_lo < t_hi) gload(t_lo);
+  for (int t = t_lo; t < t_hi; ++t) {
+    if (t > t_lo) __syncthreads();
+    if (!C::PREFETCH) gload(t);
+    lstore();
+    __syncthreads();
+    if (C::PREFETCH && t + 1 < t_hi) gload(t + 1);
+
+    const int n0 = t * C::BN;
+    const bool skip = (p.causal && n0 > mw + 31) || (p.window > 0 && mw - (n0 + C::BN - 1) > p.window);
+    if (skip) continue;
+    const bool full = (n0 + C::BN <= p.Skv) && (!p.causal || n0 + C::BN - 1 <= mw) &&
+                      (p.window == 0 || mw + 31 - n0 <= p.window);
+
+    f32x16 s[2], dp[2];
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      s[bb] = f32x16{};
+      dp[bb] = f32x16{};
+      const T* kr = sK + (32 * bb + l32) * C::P + 8 * h;
+      const T* vr = sV + (32 * bb + l32) * C::P + 8 * h;
+#pragma unroll
+      for (int kc = 0; kc < C::KC; ++kc) {
+        s[bb] = M::mma(as_v8<V8>(lds_read16(kr + 16 * kc)), qf[kc], s[bb]);
+        dp[bb] = M::mma(as_v8<V8>(lds_read16(vr + 16 * kc)), dof[kc], dp[bb]);
+      }
+    }
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
+        float tv = 0.f;
+        const float y = score_log2<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2, my_m, j, tv);
+        float pr = fast_exp2(y - lse2);
+        if (!full && !allowed(p, my_m, j)) pr = 0.f;
+        float ds = pr * (dp[bb][r] - dl) * p.scale;
+        if constexpr (SOFTCAP) ds *= (1.0f - tv * tv);
+        s[bb][r] = ds;
+      }
+    }
+    const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const V8 dsb = pack8<T>(s[bb], 8 * c);
+        const int row = 32 * bb + 16 * c + 4 * h + ((lane & 15) >> 2);
+        const T* kr = sK + row * C::P + tr_col;
+#pragma unroll
+        for (int db = 0; db < C::DB; ++db) {
+          const i16x4 lo = lds_read_tr4(kr + 32 * db);
+          const i16x4 hi = lds_read_tr4(kr + 8 * C::P + 32 * db);
+          acc[db] = M::mma(cat_tr<V8>(lo, hi), dsb, acc[db]);
+        }
+      }
+    }
+  }
+
+  if (my_m < p.Sq) {
+    T* op = (T*)a.dq.data + b * a.dq.sb + hq * a.dq.sh + (int64_t)my_m * a.dq.ss + 4 * h;
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        st_global8(op + 32 * db + 8 * i,
+                   pack4<T>(acc[db][4 * i], acc[db][4 * i + 1], acc[db][4 * i + 2], acc[db][4 * i + 3]));
+    }
+  }
+}
+
+// -------------------------------------------------------------- dK/dV kernel --
+template <class T, int D, bool SOFTCAP, bool ALIBI>
+__global__ __launch_bounds__(256) void bwd_dkdv_mfma_kernel(BwdArgs a) {
+  using C = BwdCfg<D>;
+  using M = Mfma<T>;
+  using V8 = typename M::v8;
+  __shared__ __attribute__((aligned(16))) T sQ[C::BMQ * C::P];
+  __shared__ __attribute__((aligned(16))) T sO[C::BMQ * C::P];  // dO tile
+  __shared__ __attribute__((aligned(16))) float sL[C::BMQ];      // log2-domain LSE
+  __shared__ __attribute__((aligned(16))) float sDl[C::BMQ];     // Delta
+
+  const Shape& p = a.p;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+
+  // (b, hkv, kv-tile); under a causal mask the first KV tiles carry the most
+  // query rows and are dispatched first.
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int kt = w % a.ntiles;
+  const int bh = w / a.ntiles;
+  const int hk = bh % p.Hkv, b = bh / p.Hkv;
+  const int n0 = kt * C::BNK;
+  const int nw = n0 + wave * 32;
+  const int my_n = nw + l32;
+
+  V8 kf[C::KC], vf[C::KC];
+  {
+    const T* kp = (const T*)a.k.data + b * a.k.sb + hk * a.k.sh;
+    const T* vp = (const T*)a.v.data + b * a.v.sb + hk * a.v.sh;
+    const int r = min(my_n, p.Skv - 1);
+    const T* sk = kp + (int64_t)r * a.k.ss + 8 * h;
+    const T* sv = vp + (int64_t)r * a.v.ss + 8 * h;
+#pragma unroll
+    for (int kc = 0; kc < C::KC; ++kc) {
+      i32x4 x = ld_global16(sk + 16 * kc), y = ld_global16(sv + 16 * kc);
+      if (my_n >= p.Skv) { x = i32x4{0, 0, 0, 0}; y = i32x4{0, 0, 0, 0}; }
+      kf[kc] = as_v8<V8>(x);
+      vf[kc] = as_v8<V8>(y);
+    }
+  }
+
+  int q_lo = p.causal ? n0 : 0;
+  int q_hi = p.Sq;
+  if (p.window > 0) q_hi = min(q_hi, n0 + C::BNK + p.window);
+  const int qt_lo = q_lo / C::BMQ;
+  const int qt_hi = (q_hi + C::BMQ - 1) / C::BMQ;
+  const int nq = max(0, qt_hi - qt_lo);
+  const int iters = nq * p.G;
+
+  i32x4 rq[C::CPTQ], ro[C::CPTQ];
+  float rl = 0.f, rd = 0.f;
+  auto gload = [&](int it) {
+    const int g = it / nq;
+    const int hq = hk * p.G + g;
+    const int m0 = (qt_lo + it % nq) * C::BMQ;
+    const T* qp = (const T*)a.q.data + b * a.q.sb + hq * a.q.sh;
+    const T* dop = (const T*)a.dout.data + b * a.dout.sb + hq * a.dout.sh;
+#pragma unroll
+    for (int e = 0; e < C::CPTQ; ++e) {
+      const int c = tid + e * C::NW * 64;
+      const int row = c / C::CPR, col = (c % C::CPR) * 8;
+      const int m = m0 + row;
+      const int mc = min(m, p.Sq - 1);
+      i32x4 xq = ld_global16(qp + (int64_t)mc * a.q.ss + col);
+      i32x4 xo = ld_global16(dop + (int64_t)mc * a.dout.ss + col);
+      if (m >= p.Sq) { xq = i32x4{0, 0, 0, 0}; xo = i32x4{0, 0, 0, 0}; }
+      rq[e] = xq;
+      ro[e] = xo;
+    }
+    if (tid < C::BMQ) {
+      const int m = m0 + tid;
+      rl = kPosInf;
+      rd = 0.f;
+      if (m < p.Sq) {
+        const int64_t ri = (int64_t)(b * p.Hq + hq) * p.Sq + m;
+        const float l = a.lse[ri];
+        rl = (l == kNegInf) ? kPosInf : l * kLog2e;
+        rd = a.delta[ri];
+      }
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int e = 0; e < C::CPTQ; ++e) {
+      const int c = tid + e * C::NW * 64;
+      const int row = c / C::CPR, col = (c % C::CPR) * 8;
+      *(i32x4*)&sQ[row * C::P + col] = rq[e];
+      *(i32x4*)&sO[row * C::P + col] = ro[e];
+    }
+    if (tid < C::BMQ) {
+      sL[tid] = rl;
+      sDl[tid] = rd;
+    }
+  };
+
+  f32x16 adk[C::DB], adv[C::DB];
+#pragma unroll
+  for (int db = 0; db < C::DB; ++db) {
+    adk[db] = f32x16{};
+    adv[db] = f32x16{};
+  }
+
+  if (C::PREFETCH && iters > 0) gload(0);
+  for (int it = 0; it < iters; ++it) {
+    if (it > 0) __syncthreads();
+    if (!C::PREFETCH) gload(it);
+    lstore();
+    __syncthreads();
+    if (C::PREFETCH && it + 1 < iters) gload(it + 1);
+
+    const int g = it / nq;
+    const int hq = hk * p.G + g;
+    const int mt = (qt_lo + it % nq) * C::BMQ;
+    const bool skip = (p.causal && mt + C::BMQ - 1 < nw) || (p.window > 0 && mt - (nw + 31) > p.window);
+    if (skip) continue;
+    const bool full = (!p.causal || mt >= nw + 31) && (p.window == 0 || mt + C::BMQ - 1 - nw <= p.window);
+    const float slope_log2 = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
+    const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+#pragma unroll
+    for (int mb = 0; mb < C::BMQ / 32; ++mb) {
+      f32x16 s = f32x16{}, dp = f32x16{};
+      const T* qr = sQ + (32 * mb + l32) * C::P + 8 * h;
+      const T* orr = sO + (32 * mb + l32) * C::P + 8 * h;
+#pragma unroll
+      for (int kc = 0; kc < C::KC; ++kc) {
+        s = M::mma(as_v8<V8>(lds_read16(qr + 16 * kc)), kf[kc], s);
+        dp = M::mma(as_v8<V8>(lds_read16(orr + 16 * kc)), vf[kc], dp);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int mr = 32 * mb + 8 * i + 4 * h;
+        const f32x4 L = *(const f32x4*)&sL[mr];
+        const f32x4 Dl = *(const f32x4*)&sDl[mr];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * i + j;
+          const int m = mt + mr + j;
+          float tv = 0.f;
+          const float y = score_log2<SOFTCAP, ALIBI>(s[r], p, slope_log2, m, my_n, tv);
+          float pr = fast_exp2(y - L[j]);
+          if (!full && !allowed(p, m, my_n)) pr = 0.f;
+          float ds = pr * (dp[r] - Dl[j]) * p.scale;
+          if constexpr (SOFTCAP) ds *= (1.0f - tv * tv);
+          s[r] = pr;
+          dp[r] = ds;
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const V8 pb = pack8<T>(s, 8 * c);
+        const V8 dsb = pack8<T>(dp, 8 * c);
+        const int row = 32 * mb + 16 * c + 4 * h + ((lane & 15) >> 2);
+        const T* orow = sO + row * C::P + tr_col;
+        const T* qrow = sQ + row * C::P + tr_col;
+#pragma unroll
+        for (int db = 0; db < C::DB; ++db) {
+          const i16x4 olo = lds_read_tr4(orow + 32 * db);
+          const i16x4 ohi = lds_read_tr4(orow + 8 * C::P + 32 * db);
+          adv[db] = M::mma(cat_tr<V8>(olo, ohi), pb, adv[db]);
+          const i16x4 qlo = lds_read_tr4(qrow + 32 * db);
+          const i16x4 qhi = lds_read_tr4(qrow + 8 * C::P + 32 * db);
+          adk[db] = M::mma(cat_tr<V8>(qlo, qhi), dsb, adk[db]);
+        }
+      }
+    }
+  }
+
+  if (my_n < p.Skv) {
+    T* kp = (T*)a.dk.data + b * a.dk.sb + hk * a.dk.sh + (int64_t)my_n * a.dk.ss + 4 * h;
+    T* vp = (T*)a.dv.data + b * a.dv.sb + hk * a.dv.sh + (int64_t)my_n * a.dv.ss + 4 * h;
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        st_global8(kp + 32 * db + 8 * i,
+                   pack4<T>(adk[db][4 * i], adk[db][4 * i + 1], adk[db][4 * i + 2], adk[db][4 * i + 3]));
+        st_global8(vp + 32 * db + 8 * i,
+                   pack4<T>(adv[db][4 * i], adv[db][4 * i + 1], adv[db][4 * i + 2], adv[db][4 * i + 3]));
+      }
+    }
+  }
+}
+
+template <class T, int D>
+hipError_t launch_dq_mfma(const BwdArgs& a, hipStream_t st) {
+  using C = BwdCfg<D>;
+  BwdArgs x = a;
+  x.ntiles = (a.p.Sq + C::BM - 1) / C::BM;
+  const dim3 grid(x.ntiles * a.p.B * a.p.Hq), block(C::NW * 64);
+  const bool sc = a.p.cap > 0.f, al = a.p.alibi != nullptr;
+  if (sc && al) hipLaunchKernelGGL((bwd_dq_mfma_kernel<T, D, true, true>), grid, block, 0, st, x);
+  else if (sc) hipLaunchKernelGGL((bwd_dq_mfma_kernel<T, D, true, false>), grid, block, 0, st, x);
+  else if (al) hipLaunchKernelGGL((bwd_dq_mfma_kernel<T, D, false, true>), grid, block, 0, st, x);
+  else hipLaunchKernelGGL((bwd_dq_mfma_kernel<T, D, false, false>), grid, block, 0, st, x);
+  return hipGetLastError();
+}
+
+template <class T, int D>
+hipError_t launch_dkdv_mfma(const BwdArgs& a, hipStream_t st) {
+  using C = BwdCfg<D>;
+  BwdArgs x = a;
+  x.ntiles = (a.p.Skv + C::BNK - 1) / C::BNK;
+  const dim3 grid(x.ntiles * a.p.B * a.p.Hkv), block(C::NW * 64);
+  const bool sc = a.p.cap > 0.f, al = a.p.alibi != nullptr;
+  if (sc && al) hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<T, D, true, true>), grid, block, 0, st, x);
+  else if (sc) hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<T, D, true, false>), grid, block, 0, st, x);
+  else if (al) hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<T, D, false, true>), grid, block, 0, st, x);
+  else hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<T, D, false, false>), grid, block, 0, st, x);
+  return hipGetLastError();
+}
+
+#define FLEXATT_CAT2(a, b) a##b
+#define FLEXATT_CAT(a, b) FLEXATT_CAT2(a, b)
+hipError_t FLEXATT_CAT(bwd_dq_mfma_bf16_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
+  return launch_dq_mfma<__bf16, FLEXATT_D>(a, st);
+}
+hipError_t FLEXATT_CAT(bwd_dq_mfma_f16_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
+  return launch_dq_mfma<_Float16, FLEXATT_D>(a, st);
+}
+hipError_t FLEXATT_CAT(bwd_dkdv_mfma_bf16_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
+  return launch_dkdv_mfma<__bf16, FLEXATT_D>(a, st);
+}
+hipError_t FLEXATT_CAT(bwd_dkdv_mfma_f16_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
+  return launch_dkdv_mfma<_Float16, FLEXATT_D>(a, st);
+}
+
+}  // namespace flexatt

@@ -1,0 +1,218 @@
+// extern "C" entry points of libflexatt (declared in include/flexatt.h):
+// argument checks, then dispatch to the kernel launchers by dtype and head dim.
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/flexatt.h"
+#include "flexatt_kernels.h"
+
+namespace {
+using namespace flexatt;
+
+size_t elt_size(int dt) {
+  switch (dt) {
+    case FLEXATT_F32: return 4;
+    case FLEXATT_F16:
+    case FLEXATT_BF16: return 2;
+    default: return 0;
+  }
+}
+
+int head_index(int d) {
+  switch (d) {
+    case 32: return 0;
+    case 64: return 1;
+    case 128: return 2;
+    case 256: return 3;
+    default: return -1;
+  }
+}
+
+int check_problem(const flexatt_problem* p) {
+  if (!p) return FLEXATT_EINVAL;
+  if (elt_size(p->dtype) == 0) return FLEXATT_EDTYPE;
+  if (p->batch <= 0 || p->heads_q <= 0 || p->heads_kv <= 0 || p->seqlen_q <= 0 || p->seqlen_kv <= 0)
+    return FLEXATT_EINVAL;
+  if (p->heads_q % p->heads_kv != 0) return FLEXATT_ESHAPE;
+  if (head_index(p->head_dim) < 0) return FLEXATT_EHEADDIM;
+  if (p->causal != 0 && p->causal != 1) return FLEXATT_EINVAL;
+  if (p->sliding_window < 0) return FLEXATT_EINVAL;
+  if (!(p->soft_cap >= 0.f) || !isfinite(p->soft_cap) || !isfinite(p->scale)) return FLEXATT_EINVAL;
+  // Grid sizes: tiles * B * H must fit a 1-D grid; row counts fit int32.
+  const int64_t rows_q = (int64_t)p->batch * p->heads_q * p->seqlen_q;
+  const int64_t rows_k = (int64_t)p->batch * p->heads_kv * p->seqlen_kv;
+  if (rows_q > INT32_MAX || rows_k > INT32_MAX) return FLEXATT_ESHAPE;
+  return FLEXATT_OK;
+}
+
+int check_tensor(const flexatt_tensor* t, int dt) {
+  if (!t || !t->data) return FLEXATT_EINVAL;
+  const int64_t es = (int64_t)elt_size(dt);
+  if (t->stride_d != 1) return FLEXATT_ELAYOUT;
+  if (t->stride_b < 0 || t->stride_h < 0 || t->stride_s < 0) return FLEXATT_ELAYOUT;
+  if (((uintptr_t)t->data) % 16 != 0) return FLEXATT_ELAYOUT;
+  if ((t->stride_b * es) % 16 || (t->stride_h * es) % 16 || (t->stride_s * es) % 16) return FLEXATT_ELAYOUT;
+  return FLEXATT_OK;
+}
+
+Shape make_shape(const flexatt_problem* p) {
+  Shape s;
+  s.B = p->batch;
+  s.Hq = p->heads_q;
+  s.Hkv = p->heads_kv;
+  s.G = p->heads_q / p->heads_kv;
+  s.Sq = p->seqlen_q;
+  s.Skv = p->seqlen_kv;
+  s.scale = p->scale;
+  s.scale_log2 = p->scale * kLog2e;
+  s.causal = p->causal;
+  s.window = p->sliding_window;
+  s.cap = p->soft_cap;
+  s.inv_cap = p->soft_cap > 0.f ? 1.0f / p->soft_cap : 0.f;
+  s.alibi = p->alibi_slopes;
+  return s;
+}
+
+View view(const flexatt_tensor* t) { return View{t->data, t->stride_b, t->stride_h, t->stride_s}; }
+MutView mview(const flexatt_tensor* t) { return MutView{t->data, t->stride_b, t->stride_h, t->stride_s}; }
+
+// [dtype][head index]
+const FwdLauncher kFwd[3][4] = {
+    {fwd_simt_f32_d32, fwd_simt_f32_d64, fwd_simt_f32_d128, fwd_simt_f32_d256},
+    {fwd_mfma_f16_d32, fwd_mfma_f16_d64, fwd_mfma_f16_d128, fwd_mfma_f16_d256},
+    {fwd_mfma_bf16_d32, fwd_mfma_bf16_d64, fwd_mfma_bf16_d128, fwd_mfma_bf16_d256},
+};
+const BwdLauncher kDq[3][4] = {
+    {bwd_dq_simt_f32_d32, bwd_dq_simt_f32_d64, bwd_dq_simt_f32_d128, bwd_dq_simt_f32_d256},
+    {bwd_dq_mfma_f16_d32, bwd_dq_mfma_f16_d64, bwd_dq_mfma_f16_d128, bwd_dq_mfma_f16_d256},
+    {bwd_dq_mfma_bf16_d32, bwd_dq_mfma_bf16_d64, bwd_dq_mfma_bf16_d128, bwd_dq_mfma_bf16_d256},
+};
+const BwdLauncher kDkdv[3][4] = {
+    {bwd_dkdv_simt_f32_d32, bwd_dkdv_simt_f32_d64, bwd_dkdv_simt_f32_d128, bwd_dkdv_simt_f32_d256},
+    {bwd_dkdv_mfma_f16_d32, bwd_dkdv_mfma_f16_d64, bwd_dkdv_mfma_f16_d128, bwd_dkdv_mfma_f16_d256},
+    {bwd_dkdv_mfma_bf16_d32, bwd_dkdv_mfma_bf16_d64, bwd_dkdv_mfma_bf16_d128, bwd_dkdv_mfma_bf16_d256},
+};
+
+#define FLEXATT_TRY(x)             \
+  do {                             \
+    const int rc_ = (x);           \
+    if (rc_ != FLEXATT_OK) return rc_; \
+  } while (0)
+
+int bwd_common(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+               const flexatt_tensor* v, const flexatt_tensor* dout, const float* lse, const float* delta,
+               BwdArgs& a) {
+  FLEXATT_TRY(check_problem(p));
+  FLEXATT_TRY(check_tensor(q, p->dtype));
+  FLEXATT_TRY(check_tensor(k, p->dtype));
+  FLEXATT_TRY(check_tensor(v, p->dtype));
+  FLEXATT_TRY(check_tensor(dout, p->dtype));
+  if (!lse || !delta) return FLEXATT_EINVAL;
+  a.q = view(q);
+  a.k = view(k);
+  a.v = view(v);
+  a.dout = view(dout);
+  a.lse = lse;
+  a.delta = delta;
+  a.p = make_shape(p);
+  a.ntiles = 0;
+  return FLEXATT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int flexatt_abi_version(void) { return FLEXATT_ABI_VERSION; }
+
+const char* flexatt_status_string(int status) {
+  switch (status) {
+    case FLEXATT_OK: return "ok";
+    case FLEXATT_EINVAL: return "invalid argument (null pointer, non-positive size or bad flag)";
+    case FLEXATT_EDTYPE: return "unsupported dtype (expected fp32, fp16 or bf16)";
+    case FLEXATT_EHEADDIM: return "unsupported head_dim (expected 32, 64, 128 or 256)";
+    case FLEXATT_ESHAPE: return "inconsistent shape (heads_q % heads_kv != 0 or sizes overflow)";
+    case FLEXATT_ELAYOUT: return "unsupported layout (innermost stride != 1 or rows not 16-byte aligned)";
+    default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown flexatt status";
+  }
+}
+
+int flexatt_fwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                const flexatt_tensor* v, const flexatt_tensor* o, float* lse, void* stream) {
+  FLEXATT_TRY(check_problem(p));
+  FLEXATT_TRY(check_tensor(q, p->dtype));
+  FLEXATT_TRY(check_tensor(k, p->dtype));
+  FLEXATT_TRY(check_tensor(v, p->dtype));
+  FLEXATT_TRY(check_tensor(o, p->dtype));
+  if (!lse) return FLEXATT_EINVAL;
+  FwdArgs a;
+  a.q = view(q);
+  a.k = view(k);
+  a.v = view(v);
+  a.o = mview(o);
+  a.lse = lse;
+  a.p = make_shape(p);
+  a.nqt = 0;
+  return (int)kFwd[p->dtype][head_index(p->head_dim)](a, (hipStream_t)stream);
+}
+
+int flexatt_bwd_delta(const flexatt_problem* p, const flexatt_tensor* o, const flexatt_tensor* dout,
+                      float* delta, void* stream) {
+  FLEXATT_TRY(check_problem(p));
+  FLEXATT_TRY(check_tensor(o, p->dtype));
+  FLEXATT_TRY(check_tensor(dout, p->dtype));
+  if (!delta) return FLEXATT_EINVAL;
+  DeltaArgs a;
+  a.o = view(o);
+  a.dout = view(dout);
+  a.delta = delta;
+  a.B = p->batch;
+  a.H = p->heads_q;
+  a.S = p->seqlen_q;
+  a.D = p->head_dim;
+  return (int)bwd_delta(p->dtype, a, (hipStream_t)stream);
+}
+
+int flexatt_bwd_dq(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                   const flexatt_tensor* v, const flexatt_tensor* dout, const float* lse,
+                   const float* delta, const flexatt_tensor* dq, void* stream) {
+  BwdArgs a;
+  FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
+  FLEXATT_TRY(check_tensor(dq, p->dtype));
+  a.dq = mview(dq);
+  return (int)kDq[p->dtype][head_index(p->head_dim)](a, (hipStream_t)stream);
+}
+
+int flexatt_bwd_dkdv(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                     const flexatt_tensor* v, const flexatt_tensor* dout, const float* lse,
+                     const float* delta, const flexatt_tensor* dk, const flexatt_tensor* dv,
+                     void* stream) {
+  BwdArgs a;
+  FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
+  FLEXATT_TRY(check_tensor(dk, p->dtype));
+  FLEXATT_TRY(check_tensor(dv, p->dtype));
+  a.dk = mview(dk);
+  a.dv = mview(dv);
+  return (int)kDkdv[p->dtype][head_index(p->head_dim)](a, (hipStream_t)stream);
+}
+
+int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                const flexatt_tensor* v, const flexatt_tensor* o, const flexatt_tensor* dout,
+                const float* lse, float* delta, const flexatt_tensor* dq, const flexatt_tensor* dk,
+                const flexatt_tensor* dv, void* stream) {
+  BwdArgs a;
+  FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
+  FLEXATT_TRY(check_tensor(o, p->dtype));
+  FLEXATT_TRY(check_tensor(dq, p->dtype));
+  FLEXATT_TRY(check_tensor(dk, p->dtype));
+  FLEXATT_TRY(check_tensor(dv, p->dtype));
+  FLEXATT_TRY(flexatt_bwd_delta(p, o, dout, delta, stream));
+  a.dq = mview(dq);
+  a.dk = mview(dk);
+  a.dv = mview(dv);
+  const int hi = head_index(p->head_dim);
+  FLEXATT_TRY((int)kDq[p->dtype][hi](a, (hipStream_t)stream));
+  return (int)kDkdv[p->dtype][hi](a, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,161 @@
+// Device-side building blocks shared by the flash-attention kernels (gfx950).
+//
+// Conventions used by every kernel in this library
+//  * tensors are [B, H, S, D] with element strides; the innermost stride is 1
+//    and rows start on 16-byte boundaries (the host entry points check this);
+//  * scores are kept in the log2 domain: y = x * log2(e), so softmax weights
+//    are exp2(y - m) and LSE(natural) = (m + log2(l)) * ln(2);
+//  * MFMA 32x32x16 (bf16/fp16) lane layout, verified on MI355X:
+//      A operand  lane l holds A[row = l%32][k = 8*(l/32) + t], t = 0..7
+//      B operand  lane l holds B[k = 8*(l/32) + t][col = l%32]
+//      C/D        acc[4*i + j] = C[row = 8*i + 4*(l/32) + j][col = l%32]
+//  * ds_read_b64_tr_b16, per 16-lane group: with M[r][c] the c-th 16-bit
+//    element at lane r's address, lane i receives M[4*t + i/4][i%4], t=0..3.
+//    Pointing lane r at &X[k0 + r/4][n0 + 4*(r%4)] therefore hands lane i the
+//    column X[k0 .. k0+3][n0 + i]: a transposed operand read from a row-major
+//    LDS tile.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/flexatt.h"
+
+namespace flexatt {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kPosInf = __builtin_huge_valf();
+
+// Kernel-side view of one [B, H, S, D] tensor.
+struct View {
+  const void* data;
+  int64_t sb, sh, ss;  // element strides (innermost stride is 1)
+};
+struct MutView {
+  void* data;
+  int64_t sb, sh, ss;
+};
+
+// Problem scalars shared by all kernels.
+struct Shape {
+  int B, Hq, Hkv, G, Sq, Skv;
+  float scale;        // softmax scale
+  float scale_log2;   // scale * log2(e)
+  int causal;
+  int window;         // 0 = off
+  float cap;          // 0 = off
+  float inv_cap;
+  const float* alibi;  // [Hq] or nullptr
+};
+
+// --- element traits ----------------------------------------------------------
+template <class T> struct Mfma;
+template <> struct Mfma<__bf16> {
+  typedef bf16x8 v8;
+  static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<_Float16> {
+  typedef f16x8 v8;
+  static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <class T> __device__ __forceinline__ T from_f32(float x) { return (T)x; }
+template <class T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
+
+// --- small helpers -------------------------------------------------------------
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// tanh(x) = 1 - 2 / (exp(2x) + 1); saturates correctly at +-inf of exp.
+__device__ __forceinline__ float fast_tanh(float x) {
+  float e = fast_exp2(x * (2.0f * kLog2e));
+  return 1.0f - 2.0f * fast_rcp(e + 1.0f);
+}
+
+// Value of lane l ^ 32 (the other half of the wave).
+__device__ __forceinline__ float swap_halves(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const bool lo = (threadIdx.x & 32) == 0;
+  return __uint_as_float(lo ? r[1] : r[0]);
+}
+
+__device__ __forceinline__ i32x4 ld_global16(const void* p) { return *(const i32x4*)p; }
+__device__ __forceinline__ void st_global8(void* p, i32x2 v) { *(i32x2*)p = v; }
+
+__device__ __forceinline__ i32x4 lds_read16(const void* p) {
+  return *(const __attribute__((address_space(3))) i32x4*)((__attribute__((address_space(3))) char*)p);
+}
+
+// Transposed 4 x 16-bit read (see header comment).
+__device__ __forceinline__ i16x4 lds_read_tr4(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)((__attribute__((address_space(3))) char*)p));
+}
+
+template <class V8> __device__ __forceinline__ V8 as_v8(i32x4 x) { return __builtin_bit_cast(V8, x); }
+template <class V8> __device__ __forceinline__ V8 cat_tr(i16x4 a, i16x4 b) {
+  i16x8 r = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  return __builtin_bit_cast(V8, r);
+}
+
+// Pack 8 fp32 accumulator values (acc[o..o+7]) into an MFMA operand.
+template <class T>
+__device__ __forceinline__ typename Mfma<T>::v8 pack8(const f32x16& a, int o) {
+  typename Mfma<T>::v8 r;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) r[t] = from_f32<T>(a[o + t]);
+  return r;
+}
+
+// Pack 4 fp32 values into 4 x T (8 bytes) for a store.
+template <class T>
+__device__ __forceinline__ i32x2 pack4(float a, float b, float c, float d) {
+  T v[4] = {from_f32<T>(a), from_f32<T>(b), from_f32<T>(c), from_f32<T>(d)};
+  return __builtin_bit_cast(i32x2, v);
+}
+
+// Remap the linear workgroup id so that each XCD (dispatch is round-robin over
+// the 8 XCDs) receives a contiguous range of logical work items: items that
+// share K/V then share one L2.
+__device__ __forceinline__ int xcd_remap(int w, int n) {
+  if ((n & 7) != 0) return w;
+  return (w & 7) * (n >> 3) + (w >> 3);
+}
+
+// Score transform in the log2 domain for one element: scale, soft-cap, ALiBi.
+template <bool SOFTCAP, bool ALIBI>
+__device__ __forceinline__ float score_log2(float s, const Shape& p, float slope_log2, int i, int j, float& t) {
+  float y;
+  if constexpr (SOFTCAP) {
+    t = fast_tanh(s * p.scale * p.inv_cap);
+    y = t * (p.cap * kLog2e);
+  } else {
+    y = s * p.scale_log2;
+  }
+  if constexpr (ALIBI) y += slope_log2 * (float)(i - j);
+  return y;
+}
+
+// allowed(i, j) for the masks of the path (j < Skv is the KV tail).
+__device__ __forceinline__ bool allowed(const Shape& p, int i, int j) {
+  bool ok = j < p.Skv;
+  if (p.causal) ok = ok && (j <= i);
+  if (p.window > 0) ok = ok && (i - j <= p.window);
+  return ok;
+}
+
+}  // namespace flexatt

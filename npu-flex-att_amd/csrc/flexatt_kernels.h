@@ -1,0 +1,54 @@
+// Kernel argument blocks and launcher declarations (internal to libflexatt).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "flexatt_device.h"
+
+namespace flexatt {
+
+struct FwdArgs {
+  View q, k, v;
+  MutView o;
+  float* lse;
+  Shape p;
+  int nqt;  // number of query tiles (set by the launcher)
+};
+
+struct DeltaArgs {
+  View o, dout;
+  float* delta;
+  int B, H, S, D;
+};
+
+struct BwdArgs {
+  View q, k, v, dout;
+  const float* lse;
+  const float* delta;
+  MutView dq, dk, dv;
+  Shape p;
+  int ntiles;  // number of row tiles of the kernel's grid (set by the launcher)
+};
+
+typedef hipError_t (*FwdLauncher)(const FwdArgs&, hipStream_t);
+typedef hipError_t (*BwdLauncher)(const BwdArgs&, hipStream_t);
+
+#define FLEXATT_DECL_D(D)                                                     \
+  hipError_t fwd_mfma_bf16_d##D(const FwdArgs&, hipStream_t);                 \
+  hipError_t fwd_mfma_f16_d##D(const FwdArgs&, hipStream_t);                  \
+  hipError_t bwd_dq_mfma_bf16_d##D(const BwdArgs&, hipStream_t);              \
+  hipError_t bwd_dq_mfma_f16_d##D(const BwdArgs&, hipStream_t);               \
+  hipError_t bwd_dkdv_mfma_bf16_d##D(const BwdArgs&, hipStream_t);            \
+  hipError_t bwd_dkdv_mfma_f16_d##D(const BwdArgs&, hipStream_t);             \
+  hipError_t fwd_simt_f32_d##D(const FwdArgs&, hipStream_t);                  \
+  hipError_t bwd_dq_simt_f32_d##D(const BwdArgs&, hipStream_t);               \
+  hipError_t bwd_dkdv_simt_f32_d##D(const BwdArgs&, hipStream_t);
+
+FLEXATT_DECL_D(32)
+FLEXATT_DECL_D(64)
+FLEXATT_DECL_D(128)
+FLEXATT_DECL_D(256)
+#undef FLEXATT_DECL_D
+
+hipError_t bwd_delta(int dtype, const DeltaArgs&, hipStream_t);
+
+}  // namespace flexatt

@@ -1,0 +1,294 @@
+// fp32 flash attention (forward, dQ, dK/dV) on the vector ALUs.
+//
+// The reference accepts fp32 tensors on the same entry points
+// (test/test_supplementary.py:55-63; the fp32 suites of
+// test/test_comprehensive.py) and expects fp32-exact results (tolerances down
+// to 1e-5, test/test_comprehensive.py:88).  gfx950 has no reduced-precision
+// fp32 MFMA, so the fp32 path computes exactly in fp32 FMA: one 16-lane group
+// per row, K/V (or Q/dO) tiles staged in LDS, online softmax in the natural
+// domain with expf/logf/tanhf.  Semantics are those of the MFMA kernels
+// (npu_flash_attention.py:17-166, :298-402, :407-560), including the KV tail,
+// ALiBi in backward and the in-kernel GQA group sum.
+#include "flexatt_device.h"
+#include "flexatt_kernels.h"
+
+#ifndef FLEXATT_D
+#error "FLEXATT_D (head dim) must be defined"
+#endif
+
+namespace flexatt {
+
+namespace simt {
+constexpr int kRows = 16;   // rows per workgroup (one 16-lane group each)
+constexpr int kLanes = 16;  // lanes per row
+constexpr int kTile = 32;   // rows per LDS tile
+
+__device__ __forceinline__ float group_sum(float x) {
+  x += __shfl_xor(x, 8);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 1);
+  return x;
+}
+
+// Natural-domain transformed score; t receives tanh(scale*s/cap).
+__device__ __forceinline__ float score(float s, const Shape& p, float slope, int i, int j, float& t) {
+  float x = s * p.scale;
+  if (p.cap > 0.f) {
+    t = tanhf(x * p.inv_cap);
+    x = p.cap * t;
+  }
+  if (p.alibi) x += slope * (float)(i - j);
+  return x;
+}
+}  // namespace simt
+
+template <int D>
+__global__ __launch_bounds__(256) void fwd_simt_kernel(FwdArgs a) {
+  using namespace simt;
+  constexpr int E = D / kLanes;
+  __shared__ float sK[kTile][D];
+  __shared__ float sV[kTile][D];
+  const Shape& p = a.p;
+  const int tid = threadIdx.x, rg = tid / kLanes, ln = tid % kLanes;
+  const int qt = blockIdx.x % a.nqt, bh = blockIdx.x / a.nqt;
+  const int hq = bh % p.Hq, b = bh / p.Hq, hk = hq / p.G;
+  const int m0 = qt * kRows, my_m = m0 + rg;
+  const float* qp = (const float*)a.q.data + b * a.q.sb + hq * a.q.sh;
+  const float* kp = (const float*)a.k.data + b * a.k.sb + hk * a.k.sh;
+  const float* vp = (const float*)a.v.data + b * a.v.sb + hk * a.v.sh;
+  float q[E], acc[E];
+  const int rq = min(my_m, p.Sq - 1);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    q[e] = my_m < p.Sq ? qp[(int64_t)rq * a.q.ss + ln + kLanes * e] : 0.f;
+    acc[e] = 0.f;
+  }
+  const float slope = p.alibi ? p.alibi[hq] : 0.f;
+  int kv_lo = 0, kv_hi = p.Skv;
+  if (p.causal) kv_hi = min(kv_hi, m0 + kRows);
+  if (p.window > 0) kv_lo = max(0, m0 - p.window);
+  float m_run = kNegInf, l_run = 0.f;
+  for (int n0 = (kv_lo / kTile) * kTile; n0 < kv_hi; n0 += kTile) {
+    __syncthreads();
+    for (int idx = tid; idx < kTile * D; idx += 256) {
+      const int r = idx / D, c = idx % D, n = n0 + r;
+      const int nc = min(n, p.Skv - 1);
+      sK[r][c] = n < p.Skv ? kp[(int64_t)nc * a.k.ss + c] : 0.f;
+      sV[r][c] = n < p.Skv ? vp[(int64_t)nc * a.v.ss + c] : 0.f;
+    }
+    __syncthreads();
+    float sc[kTile];
+    float mx = kNegInf;
+#pragma unroll
+    for (int jj = 0; jj < kTile; ++jj) {
+      float part = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) part = fmaf(q[e], sK[jj][ln + kLanes * e], part);
+      part = group_sum(part);
+      const int j = n0 + jj;
+      float t;
+      float x = score(part, p, slope, my_m, j, t);
+      if (!allowed(p, my_m, j)) x = kNegInf;
+      sc[jj] = x;
+      mx = fmaxf(mx, x);
+    }
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == kNegInf ? 0.f : m_new;
+    const float alpha = expf(m_run - m_use);
+    l_run *= alpha;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] *= alpha;
+#pragma unroll
+    for (int jj = 0; jj < kTile; ++jj) {
+      const float pj = expf(sc[jj] - m_use);
+      l_run += pj;
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] = fmaf(pj, sV[jj][ln + kLanes * e], acc[e]);
+    }
+    m_run = m_new;
+  }
+  if (my_m < p.Sq) {
+    const bool empty = !(l_run > 0.f);
+    float* op = (float*)a.o.data + b * a.o.sb + hq * a.o.sh + (int64_t)my_m * a.o.ss;
+#pragma unroll
+    for (int e = 0; e < E; ++e) op[ln + kLanes * e] = empty ? 0.f : acc[e] / l_run;
+    if (ln == 0) a.lse[(int64_t)(b * p.Hq + hq) * p.Sq + my_m] = empty ? kNegInf : m_run + logf(l_run);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void bwd_dq_simt_kernel(BwdArgs a) {
+  using namespace simt;
+  constexpr int E = D / kLanes;
+  __shared__ float sK[kTile][D];
+  __shared__ float sV[kTile][D];
+  const Shape& p = a.p;
+  const int tid = threadIdx.x, rg = tid / kLanes, ln = tid % kLanes;
+  const int qt = blockIdx.x % a.ntiles, bh = blockIdx.x / a.ntiles;
+  const int hq = bh % p.Hq, b = bh / p.Hq, hk = hq / p.G;
+  const int m0 = qt * kRows, my_m = m0 + rg;
+  const float* qp = (const float*)a.q.data + b * a.q.sb + hq * a.q.sh;
+  const float* dop = (const float*)a.dout.data + b * a.dout.sb + hq * a.dout.sh;
+  const float* kp = (const float*)a.k.data + b * a.k.sb + hk * a.k.sh;
+  const float* vp = (const float*)a.v.data + b * a.v.sb + hk * a.v.sh;
+  float q[E], dO[E], dq[E];
+  const int rq = min(my_m, p.Sq - 1);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    q[e] = my_m < p.Sq ? qp[(int64_t)rq * a.q.ss + ln + kLanes * e] : 0.f;
+    dO[e] = my_m < p.Sq ? dop[(int64_t)rq * a.dout.ss + ln + kLanes * e] : 0.f;
+    dq[e] = 0.f;
+  }
+  float lse = kPosInf, dl = 0.f;
+  if (my_m < p.Sq) {
+    const int64_t ri = (int64_t)(b * p.Hq + hq) * p.Sq + my_m;
+    lse = a.lse[ri] == kNegInf ? kPosInf : a.lse[ri];
+    dl = a.delta[ri];
+  }
+  const float slope = p.alibi ? p.alibi[hq] : 0.f;
+  int kv_lo = 0, kv_hi = p.Skv;
+  if (p.causal) kv_hi = min(kv_hi, m0 + kRows);
+  if (p.window > 0) kv_lo = max(0, m0 - p.window);
+  for (int n0 = (kv_lo / kTile) * kTile; n0 < kv_hi; n0 += kTile) {
+    __syncthreads();
+    for (int idx = tid; idx < kTile * D; idx += 256) {
+      const int r = idx / D, c = idx % D, n = n0 + r;
+      const int nc = min(n, p.Skv - 1);
+      sK[r][c] = n < p.Skv ? kp[(int64_t)nc * a.k.ss + c] : 0.f;
+      sV[r][c] = n < p.Skv ? vp[(int64_t)nc * a.v.ss + c] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int jj = 0; jj < kTile; ++jj) {
+      float s = 0.f, dpv = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        s = fmaf(q[e], sK[jj][ln + kLanes * e], s);
+        dpv = fmaf(dO[e], sV[jj][ln + kLanes * e], dpv);
+      }
+      s = group_sum(s);
+      dpv = group_sum(dpv);
+      const int j = n0 + jj;
+      float t = 0.f;
+      const float x = score(s, p, slope, my_m, j, t);
+      const float pj = allowed(p, my_m, j) ? expf(x - lse) : 0.f;
+      float ds = pj * (dpv - dl) * p.scale;
+      if (p.cap > 0.f) ds *= (1.0f - t * t);
+#pragma unroll
+      for (int e = 0; e < E; ++e) dq[e] = fmaf(ds, sK[jj][ln + kLanes * e], dq[e]);
+    }
+  }
+  if (my_m < p.Sq) {
+    float* op = (float*)a.dq.data + b * a.dq.sb + hq * a.dq.sh + (int64_t)my_m * a.dq.ss;
+#pragma unroll
+    for (int e = 0; e < E; ++e) op[ln + kLanes * e] = dq[e];
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void bwd_dkdv_simt_kernel(BwdArgs a) {
+  using namespace simt;
+  constexpr int E = D / kLanes;
+  __shared__ float sQ[kTile][D];
+  __shared__ float sO[kTile][D];
+  __shared__ float sL[kTile], sDl[kTile];
+  const Shape& p = a.p;
+  const int tid = threadIdx.x, rg = tid / kLanes, ln = tid % kLanes;
+  const int kt = blockIdx.x % a.ntiles, bh = blockIdx.x / a.ntiles;
+  const int hk = bh % p.Hkv, b = bh / p.Hkv;
+  const int n0 = kt * kRows, my_n = n0 + rg;
+  const float* kp = (const float*)a.k.data + b * a.k.sb + hk * a.k.sh;
+  const float* vp = (const float*)a.v.data + b * a.v.sb + hk * a.v.sh;
+  float k[E], v[E], dk[E], dv[E];
+  const int rn = min(my_n, p.Skv - 1);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    k[e] = my_n < p.Skv ? kp[(int64_t)rn * a.k.ss + ln + kLanes * e] : 0.f;
+    v[e] = my_n < p.Skv ? vp[(int64_t)rn * a.v.ss + ln + kLanes * e] : 0.f;
+    dk[e] = dv[e] = 0.f;
+  }
+  int q_lo = p.causal ? n0 : 0, q_hi = p.Sq;
+  if (p.window > 0) q_hi = min(q_hi, n0 + kRows + p.window);
+  for (int g = 0; g < p.G; ++g) {
+    const int hq = hk * p.G + g;
+    const float slope = p.alibi ? p.alibi[hq] : 0.f;
+    const float* qp = (const float*)a.q.data + b * a.q.sb + hq * a.q.sh;
+    const float* dop = (const float*)a.dout.data + b * a.dout.sb + hq * a.dout.sh;
+    for (int m0 = (q_lo / kTile) * kTile; m0 < q_hi; m0 += kTile) {
+      __syncthreads();
+      for (int idx = tid; idx < kTile * D; idx += 256) {
+        const int r = idx / D, c = idx % D, m = m0 + r;
+        const int mc = min(m, p.Sq - 1);
+        sQ[r][c] = m < p.Sq ? qp[(int64_t)mc * a.q.ss + c] : 0.f;
+        sO[r][c] = m < p.Sq ? dop[(int64_t)mc * a.dout.ss + c] : 0.f;
+      }
+      if (tid < kTile) {
+        const int m = m0 + tid;
+        float l = kPosInf, d = 0.f;
+        if (m < p.Sq) {
+          const int64_t ri = (int64_t)(b * p.Hq + hq) * p.Sq + m;
+          l = a.lse[ri] == kNegInf ? kPosInf : a.lse[ri];
+          d = a.delta[ri];
+        }
+        sL[tid] = l;
+        sDl[tid] = d;
+      }
+      __syncthreads();
+#pragma unroll 4
+      for (int ii = 0; ii < kTile; ++ii) {
+        float s = 0.f, dpv = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          s = fmaf(sQ[ii][ln + kLanes * e], k[e], s);
+          dpv = fmaf(sO[ii][ln + kLanes * e], v[e], dpv);
+        }
+        s = group_sum(s);
+        dpv = group_sum(dpv);
+        const int m = m0 + ii;
+        float t = 0.f;
+        const float x = score(s, p, slope, m, my_n, t);
+        const float pj = (m < p.Sq && allowed(p, m, my_n)) ? expf(x - sL[ii]) : 0.f;
+        float ds = pj * (dpv - sDl[ii]) * p.scale;
+        if (p.cap > 0.f) ds *= (1.0f - t * t);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          dv[e] = fmaf(pj, sO[ii][ln + kLanes * e], dv[e]);
+          dk[e] = fmaf(ds, sQ[ii][ln + kLanes * e], dk[e]);
+        }
+      }
+    }
+  }
+  if (my_n < p.Skv) {
+    float* kd = (float*)a.dk.data + b * a.dk.sb + hk * a.dk.sh + (int64_t)my_n * a.dk.ss;
+    float* vd = (float*)a.dv.data + b * a.dv.sb + hk * a.dv.sh + (int64_t)my_n * a.dv.ss;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      kd[ln + kLanes * e] = dk[e];
+      vd[ln + kLanes * e] = dv[e];
+    }
+  }
+}
+
+#define FLEXATT_CAT2(a, b) a##b
+#define FLEXATT_CAT(a, b) FLEXATT_CAT2(a, b)
+hipError_t FLEXATT_CAT(fwd_simt_f32_d, FLEXATT_D)(const FwdArgs& a, hipStream_t st) {
+  FwdArgs x = a;
+  x.nqt = (a.p.Sq + simt::kRows - 1) / simt::kRows;
+  hipLaunchKernelGGL((fwd_simt_kernel<FLEXATT_D>), dim3(x.nqt * a.p.B * a.p.Hq), dim3(256), 0, st, x);
+  return hipGetLastError();
+}
+hipError_t FLEXATT_CAT(bwd_dq_simt_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
+  BwdArgs x = a;
+  x.ntiles = (a.p.Sq + simt::kRows - 1) / simt::kRows;
+  hipLaunchKernelGGL((bwd_dq_simt_kernel<FLEXATT_D>), dim3(x.ntiles * a.p.B * a.p.Hq), dim3(256), 0, st, x);
+  return hipGetLastError();
+}
+hipError_t FLEXATT_CAT(bwd_dkdv_simt_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
+  BwdArgs x = a;
+  x.ntiles = (a.p.Skv + simt::kRows - 1) / simt::kRows;
+  hipLaunchKernelGGL((bwd_dkdv_simt_kernel<FLEXATT_D>), dim3(x.ntiles * a.p.B * a.p.Hkv), dim3(256), 0, st, x);
+  return hipGetLastError();
+}
+
+}  // namespace flexatt

@@ -1,0 +1,270 @@
+"""CPU oracle for the flash-attention forward/backward hot path.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker.  The product path (``npu_flash_attention`` and the HIP library under
+it) never imports it and has no CPU fallback.
+
+What it restates
+----------------
+The reference (dropletzhu/npu-flex-att) defines the semantics of the path in
+its Triton kernels and checks them in its tests against PyTorch eager math.
+This module is that eager math, in float64 on the CPU by default, extended to
+every primitive the kernels implement:
+
+* score order ``x = scale * q.k`` -> soft-cap ``cap*tanh(x/cap)`` -> ALiBi
+  ``+ slope[h]*(i-j)`` -> mask  (npu_flash_attention.py:102-109, :129-141);
+* mask ``allowed(i,j) = (j<=i if causal) & (i-j<=W if W>0) & (j<Skv)``
+  (npu_flash_attention.py:65-80, :138-141; the ``j<Skv`` term is the tail
+  handling the reference lacks, README.md:199);
+* softmax with natural-log LSE, fully-masked rows give ``O=0, LSE=-inf``
+  (npu_flash_attention.py:152-166);
+* GQA: query head ``h`` reads KV head ``h // G`` (npu_flash_attention.py:42);
+* backward: ``Delta = rowsum(O*dO)`` (npu_flash_attention.py:681-685),
+  ``dS = P*(dP-Delta)*scale*(1-tanh^2)`` (npu_flash_attention.py:386-399,
+  :502-516), dK/dV summed over the G query heads of a group
+  (npu_flash_attention.py:734-737).  Unlike the reference kernels, the ALiBi
+  bias is part of the recomputed P (the reference drops it in backward); the
+  oracle follows the eager autograd math, which is what the reference's tests
+  compare against (test/test_comprehensive.py:54-60).
+
+Pinning (the checks that make this module trustworthy live in
+``tests/test_oracle.py``): library SDPA equality, per-row brute-force loops,
+``torch.logsumexp``, closed forms (V=0, Q=0, S=1, dV=P^T dO, the Delta
+identity), finite-difference gradient checks and planted-mistake checks.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+__all__ = [
+    "allowed_mask",
+    "scores",
+    "forward",
+    "delta",
+    "backward",
+    "backward_autograd",
+    "forward_backward_chunked",
+    "attention_pairs",
+]
+
+
+def allowed_mask(sq: int, skv: int, causal: bool, sliding_window: int) -> torch.Tensor:
+    """Boolean [Sq, Skv] mask of attended (i, j) pairs.
+
+    Follows npu_flash_attention.py:138-141: causal keeps ``j <= i`` (top-left
+    aligned, the same as ``F.scaled_dot_product_attention(is_causal=True)``
+    used by test A14), a window ``W > 0`` keeps ``i - j <= W`` (W+1 keys when
+    causal; future keys are not masked without causal).  Columns never exceed
+    ``Skv`` here because the matrix is exactly [Sq, Skv].
+    """
+    i = torch.arange(sq).view(-1, 1)
+    j = torch.arange(skv).view(1, -1)
+    ok = torch.ones(sq, skv, dtype=torch.bool)
+    if causal:
+        ok &= j <= i
+    if sliding_window > 0:
+        ok &= (i - j) <= sliding_window
+    return ok
+
+
+def _expand_kv(x: torch.Tensor, groups: int) -> torch.Tensor:
+    """[B, Hkv, S, D] -> [B, Hkv*G, S, D]; consecutive query heads share a KV
+    head (npu_flash_attention.py:42, test/test_comprehensive.py:189)."""
+    return x if groups == 1 else x.repeat_interleave(groups, dim=1)
+
+
+def scores(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    scale: float,
+    soft_cap: float = 0.0,
+    alibi_slope: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Unmasked logits ``x`` [B, Hq, Sq, Skv] and ``tanh(scale*qk/cap)``.
+
+    Order follows npu_flash_attention.py:102-109: scale, then soft-cap, then
+    ``+ slope[h] * (i - j)`` (the reference's sign: the bias grows with
+    distance for positive slopes).  ``k`` must already be expanded to Hq heads.
+    """
+    x = torch.matmul(q, k.transpose(-2, -1)) * scale
+    t = None
+    if soft_cap > 0.0:
+        t = torch.tanh(x / soft_cap)
+        x = soft_cap * t
+    if alibi_slope is not None:
+        sq, skv = x.shape[-2], x.shape[-1]
+        i = torch.arange(sq, dtype=x.dtype).view(-1, 1)
+        j = torch.arange(skv, dtype=x.dtype).view(1, -1)
+        slope = alibi_slope.to(x.dtype).view(1, -1, 1, 1)
+        x = x + slope * (i - j)
+    return x, t
+
+
+def _prep(q, k, v, scale, dtype):
+    b, hq, sq, d = q.shape
+    hkv = k.shape[1]
+    assert hq % hkv == 0
+    g = hq // hkv
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)  # npu_flash_attention.py:625-626
+    q = q.detach().to("cpu", dtype)
+    k = _expand_kv(k.detach().to("cpu", dtype), g)
+    v = _expand_kv(v.detach().to("cpu", dtype), g)
+    return q, k, v, float(scale), g
+
+
+def _softmax_masked(x: torch.Tensor, ok: torch.Tensor):
+    """Masked softmax with natural-log LSE; fully masked rows -> P=0, LSE=-inf
+    (npu_flash_attention.py:152-161)."""
+    x = x.masked_fill(~ok, float("-inf"))
+    lse = torch.logsumexp(x, dim=-1)
+    safe = torch.where(torch.isfinite(lse), lse, torch.zeros_like(lse))
+    p = torch.exp(x - safe.unsqueeze(-1))
+    p = torch.where(ok, p, torch.zeros_like(p))
+    return p, lse
+
+
+def forward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal: bool = False,
+    sliding_window: int = 0,
+    alibi_slope: Optional[torch.Tensor] = None,
+    scale: Optional[float] = None,
+    soft_cap: float = 0.0,
+    dtype: torch.dtype = torch.float64,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Eager attention forward: returns (O [B,Hq,Sq,D], LSE [B,Hq,Sq]).
+
+    Semantics of npu_flash_attention.py:17-166 (flash_attn_fwd_kernel) as the
+    eager math of test/test_comprehensive.py:42-51 and :63-73 and
+    test/test_real_world.py:183-199 compute it, in ``dtype`` on the CPU.
+    """
+    qf, kf, vf, scale, _ = _prep(q, k, v, scale, dtype)
+    x, _ = scores(qf, kf, scale, soft_cap, alibi_slope)
+    ok = allowed_mask(x.shape[-2], x.shape[-1], causal, sliding_window)
+    p, lse = _softmax_masked(x, ok)
+    return torch.matmul(p, vf), lse
+
+
+def delta(o: torch.Tensor, do: torch.Tensor, dtype: torch.dtype = torch.float64) -> torch.Tensor:
+    """``Delta[b,h,i] = sum_d O*dO`` (npu_flash_attention.py:681-685)."""
+    return (o.detach().to("cpu", dtype) * do.detach().to("cpu", dtype)).sum(-1)
+
+
+def backward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    do: torch.Tensor,
+    causal: bool = False,
+    sliding_window: int = 0,
+    alibi_slope: Optional[torch.Tensor] = None,
+    scale: Optional[float] = None,
+    soft_cap: float = 0.0,
+    dtype: torch.dtype = torch.float64,
+    o: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Closed-form attention backward: (dQ, dK, dV), dK/dV in [B,Hkv,Skv,D].
+
+    Formulas of npu_flash_attention.py:386-399 (dQ) and :502-516 (dK/dV):
+    ``P = exp(x - LSE)``, ``dP = dO V^T``, ``Delta = rowsum(O*dO)``,
+    ``dS = P*(dP - Delta)*scale*(1 - tanh^2)``, ``dQ = dS K``,
+    ``dK = dS^T Q``, ``dV = P^T dO``, summed over each GQA group
+    (npu_flash_attention.py:734-737).  ``o`` may be given to use a specific
+    forward output for Delta (as the reference's wrapper does); by default the
+    oracle's own O is used.
+    """
+    b, hq, sq, d = q.shape
+    hkv = k.shape[1]
+    qf, kf, vf, scale, g = _prep(q, k, v, scale, dtype)
+    dof = do.detach().to("cpu", dtype)
+    x, t = scores(qf, kf, scale, soft_cap, alibi_slope)
+    ok = allowed_mask(sq, x.shape[-1], causal, sliding_window)
+    p, _ = _softmax_masked(x, ok)
+    of = torch.matmul(p, vf) if o is None else o.detach().to("cpu", dtype)
+    dl = (of * dof).sum(-1, keepdim=True)
+    dp = torch.matmul(dof, vf.transpose(-2, -1))
+    ds = p * (dp - dl)
+    if t is not None:
+        ds = ds * (1.0 - t * t)
+    ds = ds * scale
+    dq = torch.matmul(ds, kf)
+    dk = torch.matmul(ds.transpose(-2, -1), qf)
+    dv = torch.matmul(p.transpose(-2, -1), dof)
+    skv = kf.shape[2]
+    dk = dk.view(b, hkv, g, skv, d).sum(2)
+    dv = dv.view(b, hkv, g, skv, d).sum(2)
+    return dq, dk, dv
+
+
+def backward_autograd(q, k, v, do, causal=False, sliding_window=0, alibi_slope=None,
+                      scale=None, soft_cap=0.0, dtype=torch.float64):
+    """(dQ, dK, dV) by autograd through :func:`forward` — the form of the
+    reference's oracle ``ref_sdpa_backward`` (test/test_comprehensive.py:54-60);
+    GQA K/V gradients come out summed over the group because the expansion is
+    part of the graph (test/test_comprehensive.py:333-338)."""
+    qr = q.detach().to("cpu", dtype).requires_grad_(True)
+    kr = k.detach().to("cpu", dtype).requires_grad_(True)
+    vr = v.detach().to("cpu", dtype).requires_grad_(True)
+    hq, hkv = q.shape[1], k.shape[1]
+    g = hq // hkv
+    sc = (1.0 / math.sqrt(q.shape[-1])) if scale is None else float(scale)
+    x, _ = scores(qr, _expand_kv(kr, g), sc, soft_cap, alibi_slope)
+    ok = allowed_mask(x.shape[-2], x.shape[-1], causal, sliding_window)
+    p, _ = _softmax_masked(x, ok)
+    o = torch.matmul(p, _expand_kv(vr, g))
+    o.backward(do.detach().to("cpu", dtype))
+    return qr.grad, kr.grad, vr.grad
+
+
+def attention_pairs(sq: int, skv: int, causal: bool, sliding_window: int) -> int:
+    """Number of attended (i, j) pairs per head — the FLOP-count numerator."""
+    total = 0
+    for i in range(sq):
+        lo = 0
+        hi = skv - 1
+        if causal:
+            hi = min(hi, i)
+        if sliding_window > 0:
+            lo = max(lo, i - sliding_window)
+        if hi >= lo:
+            total += hi - lo + 1
+    return total
+
+
+def forward_backward_chunked(q, k, v, do, causal=False, sliding_window=0, alibi_slope=None,
+                             scale=None, soft_cap=0.0, dtype=torch.float32, with_backward=True,
+                             max_groups=None):
+    """Forward (+ backward) evaluated one (batch, KV-head group) at a time.
+
+    Bounds memory at the large configurations (the score matrix of one group
+    is G*Sq*Skv elements).  ``max_groups`` evaluates only the first N groups
+    (the bounded sample the CPU baseline times).  Returns the list of per-group
+    results ``(b, hkv, O, LSE, dQ, dK, dV)``.
+    """
+    b, hq, sq, d = q.shape
+    hkv = k.shape[1]
+    g = hq // hkv
+    out = []
+    count = 0
+    for bi in range(b):
+        for h in range(hkv):
+            if max_groups is not None and count >= max_groups:
+                return out
+            hs = slice(h * g, (h + 1) * g)
+            qs, ks, vs = q[bi:bi + 1, hs], k[bi:bi + 1, h:h + 1], v[bi:bi + 1, h:h + 1]
+            sl = None if alibi_slope is None else alibi_slope[hs]
+            o, lse = forward(qs, ks, vs, causal, sliding_window, sl, scale, soft_cap, dtype)
+            grads = (None, None, None)
+            if with_backward:
+                grads = backward(qs, ks, vs, do[bi:bi + 1, hs], causal, sliding_window, sl,
+                                 scale, soft_cap, dtype, o=o)
+            out.append((bi, h, o, lse) + tuple(grads))
+            count += 1
+    return out

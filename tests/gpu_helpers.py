@@ -1,0 +1,85 @@
+"""Helpers shared by the GPU parity tests (not collected by pytest).
+
+Inputs are drawn on the CPU from torch.Generator().manual_seed(seed) as fp32
+N(0,1) in the order q, k, v, dO, cast to the test dtype and copied to the GPU,
+so the kernels and the CPU oracle see bit-identical inputs.
+
+Tolerance criterion (stated once, used everywhere):
+    err(x, ref) = max|x - ref| / max(1, max|ref|)
+i.e. max-abs error for O(1) tensors and max-abs relative to the tensor's
+magnitude for large gradients.  The oracle runs in float64 on the same
+(rounded) inputs.
+"""
+import math
+
+import torch
+
+from oracle import attention_oracle as orc
+
+# north-star tolerances (max-abs 5e-3 fp16, 2e-2 bf16 relative to fp32) for
+# the forward; the gradients carry the extra rounding of P and dS to the input
+# dtype before their MFMAs (as in the reference kernels) and get 2x.
+TOL = {
+    torch.float32: {"o": 1e-5, "lse": 1e-5, "dq": 1e-4, "dk": 1e-4, "dv": 1e-4},
+    torch.float16: {"o": 5e-3, "lse": 1e-3, "dq": 1e-2, "dk": 1e-2, "dv": 1e-2},
+    torch.bfloat16: {"o": 2e-2, "lse": 5e-3, "dq": 4e-2, "dk": 4e-2, "dv": 4e-2},
+}
+
+
+def draw(seed, b, hq, hkv, sq, skv, d, dtype, scale_inputs=1.0, device="cuda"):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, hq, sq, d, generator=g) * scale_inputs
+    k = torch.randn(b, hkv, skv, d, generator=g) * scale_inputs
+    v = torch.randn(b, hkv, skv, d, generator=g) * scale_inputs
+    do = torch.randn(b, hq, sq, d, generator=g)
+    cpu = [t.to(dtype) for t in (q, k, v, do)]
+    return cpu, [t.to(device) for t in cpu]
+
+
+def err(x, ref):
+    x = x.detach().to("cpu", torch.float64)
+    ref = ref.detach().to("cpu", torch.float64)
+    fin = torch.isfinite(ref)
+    assert torch.equal(torch.isfinite(x), fin), "non-finite pattern differs"
+    if not bool(fin.any()):
+        return 0.0
+    d = (x[fin] - ref[fin]).abs().max().item()
+    return d / max(1.0, ref[fin].abs().max().item())
+
+
+def check(name, x, ref, dtype, report=None, factor=1.0):
+    e = err(x, ref)
+    tol = TOL[dtype][name] * factor
+    if report is not None:
+        report[name] = e
+    assert e <= tol, f"{name}: err {e:.3e} > tol {tol:.1e}"
+    return e
+
+
+def fwd_bwd(nfa, q, k, v, do, **kw):
+    o, lse = nfa.npu_flash_attention_forward(q, k, v, return_lse=True, **kw)
+    dq, dk, dv = nfa.npu_flash_attention_backward(q, k, v, o, lse, do, **kw)
+    torch.cuda.synchronize()
+    return o, lse, dq, dk, dv
+
+
+def oracle_fwd_bwd(q, k, v, do, causal=False, sliding_window=0, alibi_slope=None, scale=None, soft_cap=0.0,
+                   dtype=torch.float64):
+    sl = None if alibi_slope is None else alibi_slope.cpu()
+    o, lse = orc.forward(q, k, v, causal, sliding_window, sl, scale, soft_cap, dtype)
+    dq, dk, dv = orc.backward(q, k, v, do, causal, sliding_window, sl, scale, soft_cap, dtype)
+    return o, lse, dq, dk, dv
+
+
+def alibi_slopes(hq):
+    """Config 5's slopes 2^(-8(h+1)/Hq)."""
+    return torch.tensor([2.0 ** (-8.0 * (h + 1) / hq) for h in range(hq)], dtype=torch.float32)
+
+
+def flops(b, hq, sq, skv, d, causal, window):
+    pairs = orc.attention_pairs(sq, skv, causal, window)
+    return 4.0 * d * pairs * b * hq, 10.0 * d * pairs * b * hq
+
+
+def default_scale(d):
+    return 1.0 / math.sqrt(d)

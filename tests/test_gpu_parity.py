@@ -1,0 +1,96 @@
+"""GPU parity of the HIP kernels against the CPU oracle over the primitive grid.
+
+Every dtype x head dim x mask combination, with GQA, Sq != Skv and a KV
+length that is not a tile multiple, forward (O, LSE) and backward
+(dQ, dK, dV), through the public API (and so through the C ABI).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import npu_flash_attention as nfa
+from gpu_helpers import TOL, alibi_slopes, check, draw, fwd_bwd, oracle_fwd_bwd
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+HEAD_DIMS = [32, 64, 128, 256]
+# name: (causal, window, alibi, soft_cap, scale)
+FLAGS = {
+    "full": (False, 0, False, 0.0, None),
+    "causal": (True, 0, False, 0.0, None),
+    "causal_window": (True, 37, False, 0.0, None),
+    "window": (False, 29, False, 0.0, 0.09),
+    "causal_alibi_cap": (True, 0, True, 5.0, None),
+    "all": (True, 41, True, 3.0, 0.05),
+}
+
+
+@pytest.mark.parametrize("flags", list(FLAGS))
+@pytest.mark.parametrize("d", HEAD_DIMS)
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "fp16", "fp32"])
+def test_primitive_grid(gpu_device, dtype, d, flags):
+    causal, window, alibi, cap, scale = FLAGS[flags]
+    b, hq, hkv, sq, skv = 2, 4, 2, 200, 173
+    cpu, dev = draw(11, b, hq, hkv, sq, skv, d, dtype)
+    slopes = alibi_slopes(hq) if alibi else None
+    kw = dict(causal=causal, sliding_window=window, soft_cap=cap, scale=scale,
+              alibi_slope=None if slopes is None else slopes.to(gpu_device))
+    got = fwd_bwd(nfa, *dev, **kw)
+    ref = oracle_fwd_bwd(*cpu, causal=causal, sliding_window=window, alibi_slope=slopes, scale=scale, soft_cap=cap)
+    rep = {}
+    for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
+        check(name, x, r, dtype, rep)
+    print(f"[grid] {dtype} D={d} {flags}: " + " ".join(f"{k}={v:.2e}" for k, v in rep.items()))
+
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "attention_golden.npz")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def test_golden_config1_fp32(gpu_device, gold):
+    q, k, v, do = (torch.from_numpy(gold[f"config1/{n}"]).to(gpu_device) for n in ("q", "k", "v", "do"))
+    got = fwd_bwd(nfa, q, k, v, do, causal=True)
+    for name, x in zip(("o", "lse", "dq", "dk", "dv"), got):
+        check(name, x, torch.from_numpy(gold[f"config1/{name}"]), torch.float32)
+
+
+@pytest.mark.parametrize("name", ["combo_full", "combo_causal", "combo_causal_window", "combo_window_noncausal",
+                                  "combo_causal_alibi_cap", "combo_all"])
+def test_golden_combos_fp32(gpu_device, gold, name):
+    q, k, v, do, slopes = (torch.from_numpy(gold[f"combo/{n}"]).to(gpu_device)
+                           for n in ("q", "k", "v", "do", "alibi"))
+    causal, window, alibi, cap, scale = gold[f"{name}/flags"].tolist()
+    got = fwd_bwd(nfa, q, k, v, do, causal=bool(causal), sliding_window=int(window),
+                  alibi_slope=slopes if alibi else None, soft_cap=cap, scale=None if scale < 0 else scale)
+    for nm, x in zip(("o", "lse", "dq", "dk", "dv"), got):
+        check(nm, x, torch.from_numpy(gold[f"{name}/{nm}"]), torch.float32)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("sq,skv", [(1, 1), (16, 16), (33, 33), (65, 47), (47, 300), (300, 47), (129, 127)])
+def test_ragged_lengths(gpu_device, dtype, sq, skv):
+    cpu, dev = draw(5, 1, 2, 1, sq, skv, 64, dtype)
+    for causal, window in ((True, 0), (False, 0), (True, 9), (False, 9)):
+        got = fwd_bwd(nfa, *dev, causal=causal, sliding_window=window)
+        ref = oracle_fwd_bwd(*cpu, causal=causal, sliding_window=window)
+        for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
+            check(name, x, r, dtype)
+
+
+def test_fully_masked_rows(gpu_device):
+    # Sq > Skv with a window: rows past Skv-1+W see no key -> O=0, LSE=-inf, finite grads.
+    cpu, dev = draw(6, 1, 2, 2, 150, 40, 64, torch.bfloat16)
+    got = fwd_bwd(nfa, *dev, causal=True, sliding_window=10)
+    ref = oracle_fwd_bwd(*cpu, causal=True, sliding_window=10)
+    assert torch.all(torch.isneginf(got[1][0, :, 50:].cpu()))
+    assert torch.all(got[0][0, :, 50:].float().cpu() == 0)
+    for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
+        check(name, x, r, torch.bfloat16)
