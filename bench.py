@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--config", default="gqa_llama3_8b", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bounded CPU baseline sample budget")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run one 256 MiB device copy (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -83,6 +85,14 @@ def main():
     if alibi:
         slopes = torch.tensor([2.0 ** (-8.0 * (h + 1) / Hq) for h in range(Hq)], dtype=torch.float32, device=dev)
     kw = dict(causal=causal, sliding_window=window, soft_cap=cap, scale=scale, alibi_slope=slopes)
+
+    if args.copy_probe:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     npairs = pairs(Sq, Skv, causal, window)
     fwd_flop = 4.0 * D * npairs * B * Hq

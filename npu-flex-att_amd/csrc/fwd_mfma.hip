@@ -11,8 +11,15 @@
 //    halves and the O rescale is a per-lane scalar;
 //  * O^T = V^T P^T, with P^T taken straight from the S^T accumulators and V^T
 //    read from the row-major V tile with the LDS transpose read;
-//  * K/V tiles of 64 rows are staged in LDS; the next tile's global loads are
-//    issued into registers before the current tile is computed;
+//  * K/V tiles of 64 rows are double-buffered in LDS (one barrier per tile);
+//    the next tile's global loads are issued into registers before the current
+//    tile is computed.  Row pitches: K = D+8 elements (conflict-free 16-byte
+//    column reads), V = D+16 (conflict-free transpose reads);
+//  * two workgroups per CU (<= 256 registers per lane) so that one wave's
+//    softmax overlaps the other's MFMAs;
+//  * lazy rescale: the running max only moves when a row's max grows by more
+//    than 2^8, so O is rescaled rarely; P <= 2^8 stays exact in fp16/bf16 and
+//    the final O / l and LSE use the same max, so results are unchanged;
 //  * causal/window tiles outside a wave's rows are skipped; only tiles that
 //    straddle a mask edge or the KV tail evaluate the mask per element.
 #include "flexatt_device.h"
@@ -31,19 +38,24 @@ struct FwdCfg {
   static constexpr int BN = 64;
   static constexpr int KC = D / 16;
   static constexpr int DB = D / 32;
-  static constexpr int P = D + 8;  // LDS row pitch (elements)
+  static constexpr int KP = D + 8;   // K tile pitch (elements)
+  static constexpr int VP = D + 16;  // V tile pitch (elements)
   static constexpr int CPR = D / 8;  // 16-byte chunks per row
   static constexpr int CPT = BN * CPR / (NW * 64);  // chunks per thread per tile
-  static constexpr bool PREFETCH = D <= 128;
+  static constexpr int NBUF = D <= 128 ? 2 : 1;
+  static constexpr int SK = BN * KP, SV = BN * VP;
+  static constexpr int WPE = D <= 128 ? 2 : 1;  // waves per SIMD the register budget targets
 };
 
+constexpr float kRescaleThreshold = 8.0f;  // log2 units
+
 template <class T, int D, bool SOFTCAP, bool ALIBI>
-__global__ __launch_bounds__(256) void fwd_mfma_kernel(FwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FwdCfg<D>::WPE, FwdCfg<D>::WPE)))
+void fwd_mfma_kernel(FwdArgs a) {
   using C = FwdCfg<D>;
   using M = Mfma<T>;
   using V8 = typename M::v8;
-  __shared__ __attribute__((aligned(16))) T sK[C::BN * C::P];
-  __shared__ __attribute__((aligned(16))) T sV[C::BN * C::P];
+  __shared__ __attribute__((aligned(16))) T smem[C::NBUF * (C::SK + C::SV)];
 
   const Shape& p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -81,29 +93,28 @@ __global__ __launch_bounds__(256) void fwd_mfma_kernel(FwdArgs a) {
   const int t_lo = kv_lo / C::BN;
   const int t_hi = (kv_hi + C::BN - 1) / C::BN;
 
-  i32x4 rk[C::CPT], rv[C::CPT];
-  auto gload = [&](int t) {
+  // Next-tile staging: K(t+1) is loaded at the start of tile t and written to
+  // the free LDS buffer after the first 32-row block; V(t+1) is loaded then
+  // and written at the end of the tile.  Half a tile of registers is live.
+  i32x4 rs[C::CPT];
+  auto gload = [&](const T* base, int64_t ss, int t) {
     const int n0 = t * C::BN;
 #pragma unroll
     for (int e = 0; e < C::CPT; ++e) {
       const int c = tid + e * C::NW * 64;
       const int row = c / C::CPR, col = (c % C::CPR) * 8;
       const int n = n0 + row;
-      const int nc = min(n, p.Skv - 1);
-      i32x4 xk = ld_global16(kp + (int64_t)nc * a.k.ss + col);
-      i32x4 xv = ld_global16(vp + (int64_t)nc * a.v.ss + col);
-      if (n >= p.Skv) { xk = i32x4{0, 0, 0, 0}; xv = i32x4{0, 0, 0, 0}; }
-      rk[e] = xk;
-      rv[e] = xv;
+      i32x4 x = ld_global16(base + (int64_t)min(n, p.Skv - 1) * ss + col);
+      if (n >= p.Skv) x = i32x4{0, 0, 0, 0};
+      rs[e] = x;
     }
   };
-  auto lstore = [&]() {
+  auto lstore = [&](T* dst, int pitch) {
 #pragma unroll
     for (int e = 0; e < C::CPT; ++e) {
       const int c = tid + e * C::NW * 64;
       const int row = c / C::CPR, col = (c % C::CPR) * 8;
-      *(i32x4*)&sK[row * C::P + col] = rk[e];
-      *(i32x4*)&sV[row * C::P + col] = rv[e];
+      *(i32x4*)&dst[row * pitch + col] = rs[e];
     }
   };
 
@@ -112,77 +123,125 @@ __global__ __launch_bounds__(256) void fwd_mfma_kernel(FwdArgs a) {
   for (int db = 0; db < C::DB; ++db) acc[db] = f32x16{};
   float m_run = kNegInf, l_run = 0.f;
   const float slope_log2 = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
+  const float c2 = p.scale_log2;
+  const int tr_row = 4 * h + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  if (C::PREFETCH && t_lo < t_hi) gload(t_lo);
-  for (int t = t_lo; t < t_hi; ++t) {
-    if (t > t_lo) __syncthreads();
-    if (!C::PREFETCH) gload(t);
-    lstore();
-    __syncthreads();
-    if (C::PREFETCH && t + 1 < t_hi) gload(t + 1);
-
-    const int n0 = t * C::BN;
-    const bool skip = (p.causal && n0 > mw + 31) || (p.window > 0 && mw - (n0 + C::BN - 1) > p.window);
-    if (skip) continue;
-    const bool full = (n0 + C::BN <= p.Skv) && (!p.causal || n0 + C::BN - 1 <= mw) &&
-                      (p.window == 0 || mw + 31 - n0 <= p.window);
-
-    f32x16 s[2];
+  // One 32-row KV block: S^T, online-softmax update, O^T += V^T P^T.
+  auto block = [&](int n0, const T* sK, const T* sV, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    f32x16 s = f32x16{};
+    const T* kr = sK + l32 * C::KP + 8 * h;
 #pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
-      s[bb] = f32x16{};
-      const T* kr = sK + (32 * bb + l32) * C::P + 8 * h;
-#pragma unroll
-      for (int kc = 0; kc < C::KC; ++kc) s[bb] = M::mma(as_v8<V8>(lds_read16(kr + 16 * kc)), qf[kc], s[bb]);
-    }
+    for (int kc = 0; kc < C::KC; ++kc) s = M::mma(as_v8<V8>(lds_read16(kr + 16 * kc)), qf[kc], s);
 
+    // log2-domain scores; the fast path keeps raw scores and folds the scale
+    // into the exponent's FMA.
+    constexpr bool RAW = !SOFTCAP && !ALIBI && !MASK;
     float mx = kNegInf;
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
+    if constexpr (RAW) {
+      float hi = kNegInf, lo = __builtin_huge_valf();
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
+        hi = fmaxf(hi, s[r]);
+        lo = fminf(lo, s[r]);
+      }
+      mx = c2 >= 0.f ? hi * c2 : lo * c2;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int j = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
         float tv;
-        float y = score_log2<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2, my_m, j, tv);
-        if (!full && !allowed(p, my_m, j)) y = kNegInf;
-        s[bb][r] = y;
+        float y = score_log2<SOFTCAP, ALIBI>(s[r], p, slope_log2, my_m, j, tv);
+        if constexpr (MASK) {
+          if (!allowed(p, my_m, j)) y = kNegInf;
+        }
+        s[r] = y;
         mx = fmaxf(mx, y);
       }
     }
     mx = fmaxf(mx, swap_halves(mx));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
-    float rs = 0.f;
+    const bool grow = mx > m_run + kRescaleThreshold;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float m_new = grow ? mx : m_run;
+      const float alpha = grow ? fast_exp2(m_run - m_new) : 1.f;
+      l_run *= alpha;
 #pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
+      for (int db = 0; db < C::DB; ++db) acc[db] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = (m_run == kNegInf) ? 0.f : m_run;
+    float rsum = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = fast_exp2(s[bb][r] - m_use);
-        s[bb][r] = e;
-        rs += e;
+    for (int r = 0; r < 16; ++r) {
+      float e;
+      if constexpr (RAW) e = fast_exp2(__builtin_fmaf(s[r], c2, -m_use));
+      else e = fast_exp2(s[r] - m_use);
+      s[r] = e;
+      rsum += e;
+    }
+    l_run += rsum;
+
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const V8 pb = pack8<T>(s, 8 * c);
+      const T* vr = sV + (16 * c + tr_row) * C::VP + tr_col;
+#pragma unroll
+      for (int db = 0; db < C::DB; ++db) {
+        const i16x4 lo = lds_read_tr4(vr + 32 * db);
+        const i16x4 hi = lds_read_tr4(vr + 8 * C::VP + 32 * db);
+        acc[db] = M::mma(cat_tr<V8>(lo, hi), pb, acc[db]);
       }
     }
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
-#pragma unroll
-    for (int db = 0; db < C::DB; ++db) acc[db] *= alpha;
+  };
 
-    const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  if (t_lo < t_hi) {
+    gload(kp, a.k.ss, t_lo);
+    lstore(smem, C::KP);
+    gload(vp, a.v.ss, t_lo);
+    lstore(smem + C::SK, C::VP);
+  }
+  __syncthreads();
+  for (int t = t_lo; t < t_hi; ++t) {
+    const int cur = C::NBUF == 2 ? ((t - t_lo) & 1) : 0;
+    const bool more = t + 1 < t_hi;
+    T* sK = smem + cur * (C::SK + C::SV);
+    T* sV = sK + C::SK;
+    T* nK = smem + (cur ^ 1) * (C::SK + C::SV);
+    T* nV = nK + C::SK;
+    const int n0 = t * C::BN;
+    if constexpr (C::NBUF == 2) {
+      if (more) gload(kp, a.k.ss, t + 1);
+    }
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb) {
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const V8 pb = pack8<T>(s[bb], 8 * c);
-        const int row = 32 * bb + 16 * c + 4 * h + ((lane & 15) >> 2);
-        const T* vr = sV + row * C::P + tr_col;
-#pragma unroll
-        for (int db = 0; db < C::DB; ++db) {
-          const i16x4 lo = lds_read_tr4(vr + 32 * db);
-          const i16x4 hi = lds_read_tr4(vr + 8 * C::P + 32 * db);
-          acc[db] = M::mma(cat_tr<V8>(lo, hi), pb, acc[db]);
+      const int nb = n0 + 32 * bb;
+      const bool skip = (p.causal && nb > mw + 31) || (p.window > 0 && mw - (nb + 31) > p.window);
+      if (!skip) {
+        const bool full = (nb + 32 <= p.Skv) && (!p.causal || nb + 31 <= mw) &&
+                          (p.window == 0 || mw + 31 - nb <= p.window);
+        if (full) block(nb, sK + 32 * bb * C::KP, sV + 32 * bb * C::VP, std::false_type{});
+        else block(nb, sK + 32 * bb * C::KP, sV + 32 * bb * C::VP, std::true_type{});
+      }
+      if constexpr (C::NBUF == 2) {
+        if (bb == 0 && more) {
+          lstore(nK, C::KP);
+          gload(vp, a.v.ss, t + 1);
         }
       }
+    }
+    if constexpr (C::NBUF == 2) {
+      if (more) lstore(nV, C::VP);
+      __syncthreads();
+    } else {
+      __syncthreads();
+      if (more) {
+        gload(kp, a.k.ss, t + 1);
+        lstore(sK, C::KP);
+        gload(vp, a.v.ss, t + 1);
+        lstore(sV, C::VP);
+      }
+      __syncthreads();
     }
   }
 
