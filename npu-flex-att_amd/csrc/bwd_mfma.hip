@@ -60,7 +60,8 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) T sV[C::BN * C::P];
 
   const Shape& p = a.p;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar branches)
   const int h = lane >> 5, l32 = lane & 31;
 
   const int w = xcd_remap(blockIdx.x, gridDim.x);
@@ -219,7 +220,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_mfma_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) float sDl[C::BMQ];     // Delta
 
   const Shape& p = a.p;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar branches)
   const int h = lane >> 5, l32 = lane & 31;
 
   // (b, hkv, kv-tile); under a causal mask the first KV tiles carry the most

@@ -86,6 +86,60 @@ __device__ __forceinline__ float fast_tanh(float x) {
   return 1.0f - 2.0f * fast_rcp(e + 1.0f);
 }
 
+// acc *= s in place.  Written with tied asm operands so that a rescale under a
+// branch leaves the accumulator in its registers (a plain multiply makes the
+// register allocator copy the whole accumulator on the other path).
+__device__ __forceinline__ void scale_inplace(f32x16& a, float s) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float x = a[r];
+    asm volatile("v_mul_f32_e32 %0, %1, %0" : "+v"(x) : "v"(s));
+    a[r] = x;
+  }
+}
+
+// --- direct global -> LDS tile staging --------------------------------------
+// global_load_lds_dwordx4: lane l's 16 bytes land at LDS byte address
+// (lds_addr + 16 * l).  Issued through asm so that the compiler does not place
+// a full vmcnt(0) wait before every later LDS access; completion is tracked
+// by the caller with wait_vmcnt<N>() followed by a workgroup barrier (vector
+// memory operations retire in order, so the compiler's own waits stay valid,
+// only more conservative).
+__device__ __forceinline__ void load_lds16(const void* gptr, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ unsigned lds_addr_of(const void* p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// Swizzled, unpadded tile layouts (rows of CPR 16-byte chunks).  K tiles are
+// read with 16-byte column reads (A rows of S^T = K Q^T); V/K^T/Q^T/dO^T
+// tiles with the transpose read.  Both map logical chunk c of row r to a
+// physical chunk within the same row, so whole tiles can be copied with
+// 1 KB direct-to-LDS loads.  The maps were chosen by measured LDS throughput.
+template <int CPR>
+__device__ __forceinline__ int swz_col(int r, int c) {  // for 16-byte column reads
+  if constexpr (CPR == 4) return c ^ ((r >> 2) & 3);
+  else if constexpr (CPR == 8) return c ^ ((r >> 1) & 7);
+  else return c ^ (r & 15);
+}
+template <int CPR>
+__device__ __forceinline__ int swz_tr(int r, int c) {  // for transpose reads
+  if constexpr (CPR == 4) return c;
+  else if constexpr (CPR == 8) return (c + 4 * ((r >> 1) & 1)) & 7;
+  else return (c + 4 * r) & (CPR - 1);
+}
+template <int CPR>
+__device__ __forceinline__ int swz_tr_inv(int r, int p) {
+  if constexpr (CPR == 4) return p;
+  else if constexpr (CPR == 8) return (p - 4 * ((r >> 1) & 1)) & 7;
+  else return (p - 4 * r) & (CPR - 1);
+}
+
 // Value of lane l ^ 32 (the other half of the wave).
 __device__ __forceinline__ float swap_halves(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

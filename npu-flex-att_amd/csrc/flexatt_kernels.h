@@ -11,7 +11,8 @@ struct FwdArgs {
   MutView o;
   float* lse;
   Shape p;
-  int nqt;  // number of query tiles (set by the launcher)
+  int nqt;    // number of query tiles (set by the launcher)
+  int gpack;  // query heads per workgroup (set by the launcher)
 };
 
 struct DeltaArgs {

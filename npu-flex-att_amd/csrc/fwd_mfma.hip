@@ -4,24 +4,28 @@
 // softmax over KV tiles, O in the input dtype, LSE in fp32 natural log, the
 // score order scale -> soft-cap -> ALiBi -> mask, GQA head h -> h / G.
 //
-// Decomposition (one workgroup = 4 waves = 128 query rows of one (b, hq)):
-//  * each wave owns 32 query rows and computes S^T = K Q^T per 32x32 block
-//    (A = K rows from LDS, B = its Q rows held in registers), so every lane
-//    holds one query row: the row max needs one exchange between the two wave
-//    halves and the O rescale is a per-lane scalar;
+// Decomposition
+//  * One workgroup = NW waves = one (batch, KV head) pair, a group of gp query
+//    heads that share that KV head (gp = the largest power of two dividing G,
+//    at most NW), and 32 * NW / gp query rows of each of them.  Every K/V tile
+//    brought on chip therefore serves gp heads at once (GQA is indexed
+//    directly: no K/V expansion, and gp times less L2->LDS traffic).
+//  * Each wave owns 32 query rows of one head and computes S^T = K Q^T per
+//    32x32 block (A = K rows from LDS, B = its Q rows held in registers), so
+//    every lane holds one query row: the row max needs one exchange between
+//    the two wave halves and the O rescale is a per-lane scalar.
 //  * O^T = V^T P^T, with P^T taken straight from the S^T accumulators and V^T
-//    read from the row-major V tile with the LDS transpose read;
-//  * K/V tiles of 64 rows are double-buffered in LDS (one barrier per tile);
-//    the next tile's global loads are issued into registers before the current
-//    tile is computed.  Row pitches: K = D+8 elements (conflict-free 16-byte
-//    column reads), V = D+16 (conflict-free transpose reads);
-//  * two workgroups per CU (<= 256 registers per lane) so that one wave's
-//    softmax overlaps the other's MFMAs;
-//  * lazy rescale: the running max only moves when a row's max grows by more
+//    read from the row-major V tile with the LDS transpose read.
+//  * K/V tiles are copied global -> LDS with direct-to-LDS loads into three
+//    stages, two tiles ahead of the tile being computed (no staging
+//    registers, one barrier per tile).  Tiles are unpadded with a per-row
+//    chunk swizzle (swz_col for K, swz_tr for V).
+//  * Lazy rescale: the running max only moves when a row's max grows by more
 //    than 2^8, so O is rescaled rarely; P <= 2^8 stays exact in fp16/bf16 and
-//    the final O / l and LSE use the same max, so results are unchanged;
-//  * causal/window tiles outside a wave's rows are skipped; only tiles that
-//    straddle a mask edge or the KV tail evaluate the mask per element.
+//    the final O / l and LSE use the same max, so results are unchanged.
+//  * Blocks above a wave's causal diagonal or outside its window are skipped;
+//    only blocks that straddle a mask edge or the KV tail evaluate the mask
+//    per element.
 #include "flexatt_device.h"
 #include "flexatt_kernels.h"
 
@@ -33,42 +37,48 @@ namespace flexatt {
 
 template <int D>
 struct FwdCfg {
-  static constexpr int NW = 4;
-  static constexpr int BM = 32 * NW;
-  static constexpr int BN = 64;
+  static constexpr int NW = D <= 128 ? 8 : 4;   // waves per workgroup
+  static constexpr int WPE = D <= 128 ? 2 : 1;  // waves per SIMD the register budget targets
+  static constexpr int BN = D == 32 ? 128 : (D == 256 ? 32 : 64);  // KV rows per tile
+  static constexpr int NB = BN / 32;
   static constexpr int KC = D / 16;
   static constexpr int DB = D / 32;
-  static constexpr int KP = D + 8;   // K tile pitch (elements)
-  static constexpr int VP = D + 16;  // V tile pitch (elements)
-  static constexpr int CPR = D / 8;  // 16-byte chunks per row
-  static constexpr int CPT = BN * CPR / (NW * 64);  // chunks per thread per tile
-  static constexpr int NBUF = D <= 128 ? 2 : 1;
-  static constexpr int SK = BN * KP, SV = BN * VP;
-  static constexpr int WPE = D <= 128 ? 2 : 1;  // waves per SIMD the register budget targets
+  static constexpr int CPR = D / 8;         // 16-byte chunks per row
+  static constexpr int ROWB = D * 2;        // bytes per tile row
+  static constexpr int TILEB = BN * ROWB;   // bytes per tile of one tensor
+  static constexpr int E = TILEB / (1024 * NW);  // 1 KB loads per wave per tensor per tile
+  static constexpr int STAGES = 3;
+  static_assert(E >= 1 && E * 1024 * NW == TILEB, "tile must split into 1 KB loads per wave");
 };
 
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
 
 template <class T, int D, bool SOFTCAP, bool ALIBI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FwdCfg<D>::WPE, FwdCfg<D>::WPE)))
+__global__ __launch_bounds__(FwdCfg<D>::NW * 64) __attribute__((amdgpu_waves_per_eu(FwdCfg<D>::WPE, FwdCfg<D>::WPE)))
 void fwd_mfma_kernel(FwdArgs a) {
   using C = FwdCfg<D>;
   using M = Mfma<T>;
   using V8 = typename M::v8;
-  __shared__ __attribute__((aligned(16))) T smem[C::NBUF * (C::SK + C::SV)];
+  __shared__ __attribute__((aligned(1024))) char smem[C::STAGES * 2 * C::TILEB];
 
   const Shape& p = a.p;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar branches)
   const int h = lane >> 5, l32 = lane & 31;
 
-  // (b, hq, q-tile); the longest causal tiles are dispatched first.
+  // Work item: (b, hkv, head group, q-tile); the longest causal tiles first.
+  const int gp = a.gpack;
+  const int bmh = 32 * (C::NW / gp);  // query rows per head
   const int w = xcd_remap(blockIdx.x, gridDim.x);
   const int qt = a.nqt - 1 - (w % a.nqt);
-  const int bh = w / a.nqt;
-  const int hq = bh % p.Hq, b = bh / p.Hq;
-  const int hk = hq / p.G;
-  const int m0 = qt * C::BM;
-  const int mw = m0 + wave * 32;
+  int rest = w / a.nqt;
+  const int ngs = p.G / gp;
+  const int gs = rest % ngs;
+  rest /= ngs;
+  const int hk = rest % p.Hkv, b = rest / p.Hkv;
+  const int hq = hk * p.G + gs * gp + wave % gp;
+  const int m0 = qt * bmh;
+  const int mw = m0 + 32 * (wave / gp);
   const int my_m = mw + l32;
 
   const T* qp = (const T*)a.q.data + b * a.q.sb + hq * a.q.sh;
@@ -88,35 +98,37 @@ void fwd_mfma_kernel(FwdArgs a) {
   }
 
   int kv_lo = 0, kv_hi = p.Skv;
-  if (p.causal) kv_hi = min(kv_hi, m0 + C::BM);
+  if (p.causal) kv_hi = min(kv_hi, m0 + bmh);
   if (p.window > 0) kv_lo = max(0, m0 - p.window);
   const int t_lo = kv_lo / C::BN;
   const int t_hi = (kv_hi + C::BN - 1) / C::BN;
 
-  // Next-tile staging: K(t+1) is loaded at the start of tile t and written to
-  // the free LDS buffer after the first 32-row block; V(t+1) is loaded then
-  // and written at the end of the tile.  Half a tile of registers is live.
-  i32x4 rs[C::CPT];
-  auto gload = [&](const T* base, int64_t ss, int t) {
+  // Direct global -> LDS copy of tile t into stage st: E 1 KB loads per
+  // tensor per wave; lane l of load e covers physical chunk q of the tile.
+  const unsigned lds0 = lds_addr_of(smem);
+  auto issue = [&](int t, int st) {
     const int n0 = t * C::BN;
+    const unsigned sbase = lds0 + st * 2 * C::TILEB;
 #pragma unroll
-    for (int e = 0; e < C::CPT; ++e) {
-      const int c = tid + e * C::NW * 64;
-      const int row = c / C::CPR, col = (c % C::CPR) * 8;
-      const int n = n0 + row;
-      i32x4 x = ld_global16(base + (int64_t)min(n, p.Skv - 1) * ss + col);
-      if (n >= p.Skv) x = i32x4{0, 0, 0, 0};
-      rs[e] = x;
+    for (int e = 0; e < C::E; ++e) {
+      const int blk = wave * C::E + e;
+      const int q = blk * 64 + lane;
+      const int row = q / C::CPR, pc = q % C::CPR;
+      const int64_t n = min(n0 + row, p.Skv - 1);
+      load_lds16(kp + n * a.k.ss + swz_col<C::CPR>(row, pc) * 8, sbase + blk * 1024);
+      load_lds16(vp + n * a.v.ss + swz_tr_inv<C::CPR>(row, pc) * 8, sbase + C::TILEB + blk * 1024);
     }
   };
-  auto lstore = [&](T* dst, int pitch) {
+
+  // Lane-constant byte offsets of this lane's LDS reads inside a tile.
+  int koff[C::KC], voff[C::DB];
+  const int tr_row = 4 * h + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
-    for (int e = 0; e < C::CPT; ++e) {
-      const int c = tid + e * C::NW * 64;
-      const int row = c / C::CPR, col = (c % C::CPR) * 8;
-      *(i32x4*)&dst[row * pitch + col] = rs[e];
-    }
-  };
+  for (int kc = 0; kc < C::KC; ++kc) koff[kc] = l32 * C::ROWB + swz_col<C::CPR>(l32, 2 * kc + h) * 16;
+#pragma unroll
+  for (int db = 0; db < C::DB; ++db)
+    voff[db] = tr_row * C::ROWB + swz_tr<C::CPR>(tr_row, 4 * db + (tr_col >> 3)) * 16 + (tr_col & 7) * 2;
 
   f32x16 acc[C::DB];
 #pragma unroll
@@ -124,29 +136,30 @@ void fwd_mfma_kernel(FwdArgs a) {
   float m_run = kNegInf, l_run = 0.f;
   const float slope_log2 = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
   const float c2 = p.scale_log2;
-  const int tr_row = 4 * h + ((lane & 15) >> 2);
-  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   // One 32-row KV block: S^T, online-softmax update, O^T += V^T P^T.
-  auto block = [&](int n0, const T* sK, const T* sV, auto mask_tag) {
+  auto block = [&](int n0, const char* sK, const char* sV, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     f32x16 s = f32x16{};
-    const T* kr = sK + l32 * C::KP + 8 * h;
 #pragma unroll
-    for (int kc = 0; kc < C::KC; ++kc) s = M::mma(as_v8<V8>(lds_read16(kr + 16 * kc)), qf[kc], s);
+    for (int kc = 0; kc < C::KC; ++kc) s = M::mma(as_v8<V8>(lds_read16(sK + koff[kc])), qf[kc], s);
 
     // log2-domain scores; the fast path keeps raw scores and folds the scale
     // into the exponent's FMA.
     constexpr bool RAW = !SOFTCAP && !ALIBI && !MASK;
     float mx = kNegInf;
     if constexpr (RAW) {
-      float hi = kNegInf, lo = __builtin_huge_valf();
+      if (c2 >= 0.f) {
+        float hi = kNegInf;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        hi = fmaxf(hi, s[r]);
-        lo = fminf(lo, s[r]);
+        for (int r = 0; r < 16; ++r) hi = fmaxf(hi, s[r]);
+        mx = hi * c2;
+      } else {
+        float lo = __builtin_huge_valf();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) lo = fminf(lo, s[r]);
+        mx = lo * c2;
       }
-      mx = c2 >= 0.f ? hi * c2 : lo * c2;
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -167,7 +180,7 @@ void fwd_mfma_kernel(FwdArgs a) {
       const float alpha = grow ? fast_exp2(m_run - m_new) : 1.f;
       l_run *= alpha;
 #pragma unroll
-      for (int db = 0; db < C::DB; ++db) acc[db] *= alpha;
+      for (int db = 0; db < C::DB; ++db) scale_inplace(acc[db], alpha);
       m_run = m_new;
     }
     const float m_use = (m_run == kNegInf) ? 0.f : m_run;
@@ -185,64 +198,41 @@ void fwd_mfma_kernel(FwdArgs a) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const V8 pb = pack8<T>(s, 8 * c);
-      const T* vr = sV + (16 * c + tr_row) * C::VP + tr_col;
+      const char* vr = sV + 16 * c * C::ROWB;
 #pragma unroll
       for (int db = 0; db < C::DB; ++db) {
-        const i16x4 lo = lds_read_tr4(vr + 32 * db);
-        const i16x4 hi = lds_read_tr4(vr + 8 * C::VP + 32 * db);
+        const i16x4 lo = lds_read_tr4(vr + voff[db]);
+        const i16x4 hi = lds_read_tr4(vr + 8 * C::ROWB + voff[db]);
         acc[db] = M::mma(cat_tr<V8>(lo, hi), pb, acc[db]);
       }
     }
   };
 
-  if (t_lo < t_hi) {
-    gload(kp, a.k.ss, t_lo);
-    lstore(smem, C::KP);
-    gload(vp, a.v.ss, t_lo);
-    lstore(smem + C::SK, C::VP);
-  }
-  __syncthreads();
+  if (t_lo < t_hi) issue(t_lo, 0);
+  if (t_lo + 1 < t_hi) issue(t_lo + 1, 1);
+  int st = 0;
   for (int t = t_lo; t < t_hi; ++t) {
-    const int cur = C::NBUF == 2 ? ((t - t_lo) & 1) : 0;
-    const bool more = t + 1 < t_hi;
-    T* sK = smem + cur * (C::SK + C::SV);
-    T* sV = sK + C::SK;
-    T* nK = smem + (cur ^ 1) * (C::SK + C::SV);
-    T* nV = nK + C::SK;
+    if (t + 1 < t_hi) wait_vmcnt<2 * C::E>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    if (t + 2 < t_hi) issue(t + 2, st == 0 ? 2 : st - 1);
+    const char* sK = smem + st * 2 * C::TILEB;
+    const char* sV = sK + C::TILEB;
     const int n0 = t * C::BN;
-    if constexpr (C::NBUF == 2) {
-      if (more) gload(kp, a.k.ss, t + 1);
-    }
 #pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
+    for (int bb = 0; bb < C::NB; ++bb) {
       const int nb = n0 + 32 * bb;
       const bool skip = (p.causal && nb > mw + 31) || (p.window > 0 && mw - (nb + 31) > p.window);
       if (!skip) {
         const bool full = (nb + 32 <= p.Skv) && (!p.causal || nb + 31 <= mw) &&
                           (p.window == 0 || mw + 31 - nb <= p.window);
-        if (full) block(nb, sK + 32 * bb * C::KP, sV + 32 * bb * C::VP, std::false_type{});
-        else block(nb, sK + 32 * bb * C::KP, sV + 32 * bb * C::VP, std::true_type{});
-      }
-      if constexpr (C::NBUF == 2) {
-        if (bb == 0 && more) {
-          lstore(nK, C::KP);
-          gload(vp, a.v.ss, t + 1);
-        }
+        const char* kb = sK + 32 * bb * C::ROWB;
+        const char* vb = sV + 32 * bb * C::ROWB;
+        if (full) block(nb, kb, vb, std::false_type{});
+        else block(nb, kb, vb, std::true_type{});
       }
     }
-    if constexpr (C::NBUF == 2) {
-      if (more) lstore(nV, C::VP);
-      __syncthreads();
-    } else {
-      __syncthreads();
-      if (more) {
-        gload(kp, a.k.ss, t + 1);
-        lstore(sK, C::KP);
-        gload(vp, a.v.ss, t + 1);
-        lstore(sV, C::VP);
-      }
-      __syncthreads();
-    }
+    st = st == 2 ? 0 : st + 1;
   }
 
   const float l_tot = l_run + swap_halves(l_run);
@@ -263,12 +253,20 @@ void fwd_mfma_kernel(FwdArgs a) {
   }
 }
 
+// Heads per workgroup: the largest power of two that divides G, capped at NW.
+inline int gqa_pack(int G, int nw) {
+  const int gp = G & (-G);
+  return gp < nw ? gp : nw;
+}
+
 template <class T, int D>
 hipError_t launch_fwd_mfma(const FwdArgs& a, hipStream_t st) {
   using C = FwdCfg<D>;
   FwdArgs x = a;
-  x.nqt = (a.p.Sq + C::BM - 1) / C::BM;
-  const dim3 grid(x.nqt * a.p.B * a.p.Hq), block(C::NW * 64);
+  x.gpack = gqa_pack(a.p.G, C::NW);
+  const int bmh = 32 * (C::NW / x.gpack);
+  x.nqt = (a.p.Sq + bmh - 1) / bmh;
+  const dim3 grid(x.nqt * (a.p.G / x.gpack) * a.p.B * a.p.Hkv), block(C::NW * 64);
   const bool sc = a.p.cap > 0.f, al = a.p.alibi != nullptr;
   if (sc && al) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true, true>), grid, block, 0, st, x);
   else if (sc) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true, false>), grid, block, 0, st, x);
