@@ -23,9 +23,9 @@
 //  * Lazy rescale: the running max only moves when a row's max grows by more
 //    than 2^8, so O is rescaled rarely; P <= 2^8 stays exact in fp16/bf16 and
 //    the final O / l and LSE use the same max, so results are unchanged.
-//  * Blocks above a wave's causal diagonal or outside its window are skipped;
-//    only blocks that straddle a mask edge or the KV tail evaluate the mask
-//    per element.
+//  * Only tiles that straddle a mask edge or the KV tail evaluate the mask per
+//    element; fully masked blocks of such tiles run the same instructions
+//    with P = 0 (one straight path keeps the accumulators in place).
 #include "flexatt_device.h"
 #include "flexatt_kernels.h"
 
@@ -135,44 +135,59 @@ void fwd_mfma_kernel(FwdArgs a) {
   for (int db = 0; db < C::DB; ++db) acc[db] = f32x16{};
   float m_run = kNegInf, l_run = 0.f;
   const float slope_log2 = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
-  const float c2 = p.scale_log2;
 
-  // One 32-row KV block: S^T, online-softmax update, O^T += V^T P^T.
-  auto block = [&](int n0, const char* sK, const char* sV, auto mask_tag) {
-    constexpr bool MASK = decltype(mask_tag)::value;
+  // Raw-score fast path: scores stay unscaled and the scale is folded into
+  // the exp2 FMA; a zero scale is replaced by a tiny one so that masked
+  // scores (+-inf) still map to exp2(-inf) = 0.
+  constexpr bool RAW = !SOFTCAP && !ALIBI;
+  const float c2 = p.scale_log2 != 0.f ? p.scale_log2 : 1e-30f;
+  const float masked_raw = c2 > 0.f ? kNegInf : kPosInf;
+
+  // One 32-row KV block: S^T, online-softmax update, O^T += V^T P^T.  Every
+  // block follows the same instruction path (the mask is a branch that only
+  // rewrites the score registers), so the accumulators stay in place.
+  auto block = [&](int n0, const char* sK, const char* sV, bool need_mask) {
     f32x16 s = f32x16{};
 #pragma unroll
     for (int kc = 0; kc < C::KC; ++kc) s = M::mma(as_v8<V8>(lds_read16(sK + koff[kc])), qf[kc], s);
 
-    // log2-domain scores; the fast path keeps raw scores and folds the scale
-    // into the exponent's FMA.
-    constexpr bool RAW = !SOFTCAP && !ALIBI && !MASK;
-    float mx = kNegInf;
+    float mx;
     if constexpr (RAW) {
-      if (c2 >= 0.f) {
-        float hi = kNegInf;
+      if (need_mask) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) hi = fmaxf(hi, s[r]);
-        mx = hi * c2;
-      } else {
-        float lo = __builtin_huge_valf();
-#pragma unroll
-        for (int r = 0; r < 16; ++r) lo = fminf(lo, s[r]);
-        mx = lo * c2;
+        for (int r = 0; r < 16; ++r) {
+          const int j = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (!allowed(p, my_m, j)) s[r] = masked_raw;
+        }
       }
+      float e = s[0];
+      if (c2 > 0.f) {
+#pragma unroll
+        for (int r = 1; r < 16; ++r) e = fmaxf(e, s[r]);
+      } else {
+#pragma unroll
+        for (int r = 1; r < 16; ++r) e = fminf(e, s[r]);
+      }
+      mx = e * c2;  // -inf for a fully masked block
     } else {
+      mx = kNegInf;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int j = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
         float tv;
-        float y = score_log2<SOFTCAP, ALIBI>(s[r], p, slope_log2, my_m, j, tv);
-        if constexpr (MASK) {
-          if (!allowed(p, my_m, j)) y = kNegInf;
-        }
-        s[r] = y;
-        mx = fmaxf(mx, y);
+        s[r] = score_log2<SOFTCAP, ALIBI>(s[r], p, slope_log2, my_m, j, tv);
       }
+      if (need_mask) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (!allowed(p, my_m, j)) s[r] = kNegInf;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
     }
+    if (mx != mx) mx = kNegInf;  // (+-inf) * tiny scale of a fully masked block
     mx = fmaxf(mx, swap_halves(mx));
     const bool grow = mx > m_run + kRescaleThreshold;
     if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -219,19 +234,13 @@ void fwd_mfma_kernel(FwdArgs a) {
     const char* sK = smem + st * 2 * C::TILEB;
     const char* sV = sK + C::TILEB;
     const int n0 = t * C::BN;
+    // Per element masking only on tiles that cut the causal diagonal, the
+    // window edge or the KV tail for some row of this wave.
+    const bool need_mask = (n0 + C::BN > p.Skv) || (p.causal && n0 + C::BN - 1 > mw) ||
+                           (p.window > 0 && mw + 31 - n0 > p.window);
 #pragma unroll
-    for (int bb = 0; bb < C::NB; ++bb) {
-      const int nb = n0 + 32 * bb;
-      const bool skip = (p.causal && nb > mw + 31) || (p.window > 0 && mw - (nb + 31) > p.window);
-      if (!skip) {
-        const bool full = (nb + 32 <= p.Skv) && (!p.causal || nb + 31 <= mw) &&
-                          (p.window == 0 || mw + 31 - nb <= p.window);
-        const char* kb = sK + 32 * bb * C::ROWB;
-        const char* vb = sV + 32 * bb * C::ROWB;
-        if (full) block(nb, kb, vb, std::false_type{});
-        else block(nb, kb, vb, std::true_type{});
-      }
-    }
+    for (int bb = 0; bb < C::NB; ++bb)
+      block(n0 + 32 * bb, sK + 32 * bb * C::ROWB, sV + 32 * bb * C::ROWB, need_mask);
     st = st == 2 ? 0 : st + 1;
   }
 
