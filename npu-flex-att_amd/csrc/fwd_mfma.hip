@@ -39,7 +39,11 @@ template <int D>
 struct FwdCfg {
   static constexpr int NW = D <= 128 ? 8 : 4;   // waves per workgroup
   static constexpr int WPE = D <= 128 ? 2 : 1;  // waves per SIMD the register budget targets
+#ifdef FLEXATT_FWD_BN
+  static constexpr int BN = FLEXATT_FWD_BN;  // tuning override
+#else
   static constexpr int BN = D == 32 ? 128 : (D == 256 ? 32 : 64);  // KV rows per tile
+#endif
   static constexpr int NB = BN / 32;
   static constexpr int KC = D / 16;
   static constexpr int DB = D / 32;
@@ -136,59 +140,80 @@ void fwd_mfma_kernel(FwdArgs a) {
   float m_run = kNegInf, l_run = 0.f;
   const float slope_log2 = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
 
-  // Raw-score fast path: scores stay unscaled and the scale is folded into
-  // the exp2 FMA; a zero scale is replaced by a tiny one so that masked
-  // scores (+-inf) still map to exp2(-inf) = 0.
+  // Raw-score fast path (no soft-cap, no ALiBi): scores stay unscaled and
+  // the scale is folded into the exp2 FMA.  A negative scale is moved into
+  // the sign of Q (exact), a zero scale replaced by a tiny one, so that the
+  // row max is always a max and masked scores (-inf) map to exp2(-inf) = 0.
   constexpr bool RAW = !SOFTCAP && !ALIBI;
-  const float c2 = p.scale_log2 != 0.f ? p.scale_log2 : 1e-30f;
-  const float masked_raw = c2 > 0.f ? kNegInf : kPosInf;
-
-  // One 32-row KV block: S^T, online-softmax update, O^T += V^T P^T.  Every
-  // block follows the same instruction path (the mask is a branch that only
-  // rewrites the score registers), so the accumulators stay in place.
-  auto block = [&](int n0, const char* sK, const char* sV, bool need_mask) {
-    f32x16 s = f32x16{};
+  float c2 = p.scale_log2;
+  if constexpr (RAW) {
+    if (c2 < 0.f) {
 #pragma unroll
-    for (int kc = 0; kc < C::KC; ++kc) s = M::mma(as_v8<V8>(lds_read16(sK + koff[kc])), qf[kc], s);
-
-    float mx;
-    if constexpr (RAW) {
-      if (need_mask) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int j = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (!allowed(p, my_m, j)) s[r] = masked_raw;
-        }
-      }
-      float e = s[0];
-      if (c2 > 0.f) {
-#pragma unroll
-        for (int r = 1; r < 16; ++r) e = fmaxf(e, s[r]);
-      } else {
-#pragma unroll
-        for (int r = 1; r < 16; ++r) e = fminf(e, s[r]);
-      }
-      mx = e * c2;  // -inf for a fully masked block
-    } else {
-      mx = kNegInf;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int j = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
-        float tv;
-        s[r] = score_log2<SOFTCAP, ALIBI>(s[r], p, slope_log2, my_m, j, tv);
-      }
-      if (need_mask) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int j = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (!allowed(p, my_m, j)) s[r] = kNegInf;
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+      for (int kc = 0; kc < C::KC; ++kc)
+        qf[kc] = as_v8<V8>(__builtin_bit_cast(i32x4, qf[kc]) ^ i32x4{(int)0x80008000, (int)0x80008000,
+                                                                     (int)0x80008000, (int)0x80008000});
+      c2 = -c2;
     }
-    if (mx != mx) mx = kNegInf;  // (+-inf) * tiny scale of a fully masked block
+    if (c2 == 0.f) c2 = 1e-30f;
+  }
+
+  auto tile_body = [&](const char* sK, const char* sV, int n0, bool need_mask) {
+    // S^T for every 32-row block of the tile.
+    f32x16 s[C::NB];
+#pragma unroll
+    for (int bb = 0; bb < C::NB; ++bb) {
+      s[bb] = f32x16{};
+#pragma unroll
+      for (int kc = 0; kc < C::KC; ++kc)
+        s[bb] = M::mma(as_v8<V8>(lds_read16(sK + bb * 32 * C::ROWB + koff[kc])), qf[kc], s[bb]);
+    }
+    // keep the K reads a few ahead of the MFMAs that consume them
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < C::NB * C::KC - 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+
+    // scores -> log2 domain (transform paths), mask (edge tiles only)
+    if constexpr (!RAW) {
+#pragma unroll
+      for (int bb = 0; bb < C::NB; ++bb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
+          float tv;
+          s[bb][r] = score_log2<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2, my_m, j, tv);
+        }
+    }
+    if (need_mask) {
+#pragma unroll
+      for (int bb = 0; bb < C::NB; ++bb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (!allowed(p, my_m, j)) s[bb][r] = kNegInf;
+        }
+    }
+
+    // tile row max (pairwise tree), exchanged between the wave halves
+    float mx;
+    {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = fmaxf(s[0][2 * i], s[0][2 * i + 1]);
+#pragma unroll
+      for (int bb = 1; bb < C::NB; ++bb)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = fmaxf(v[i], fmaxf(s[bb][2 * i], s[bb][2 * i + 1]));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], v[i + 4]);
+      mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+    }
+    if constexpr (RAW) mx *= c2;
     mx = fmaxf(mx, swap_halves(mx));
+    if (mx != mx) mx = kNegInf;
     const bool grow = mx > m_run + kRescaleThreshold;
     if (__builtin_amdgcn_ballot_w64(grow)) {
       const float m_new = grow ? mx : m_run;
@@ -199,27 +224,40 @@ void fwd_mfma_kernel(FwdArgs a) {
       m_run = m_new;
     }
     const float m_use = (m_run == kNegInf) ? 0.f : m_run;
-    float rsum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float e;
-      if constexpr (RAW) e = fast_exp2(__builtin_fmaf(s[r], c2, -m_use));
-      else e = fast_exp2(s[r] - m_use);
-      s[r] = e;
-      rsum += e;
-    }
-    l_run += rsum;
 
+    // P = exp2(y - m), row sums, O^T += V^T P^T
+    float rs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const V8 pb = pack8<T>(s, 8 * c);
-      const char* vr = sV + 16 * c * C::ROWB;
+    for (int bb = 0; bb < C::NB; ++bb) {
+      f32x16 e;
 #pragma unroll
-      for (int db = 0; db < C::DB; ++db) {
-        const i16x4 lo = lds_read_tr4(vr + voff[db]);
-        const i16x4 hi = lds_read_tr4(vr + 8 * C::ROWB + voff[db]);
-        acc[db] = M::mma(cat_tr<V8>(lo, hi), pb, acc[db]);
+      for (int r = 0; r < 16; ++r) {
+        if constexpr (RAW) e[r] = fast_exp2(__builtin_fmaf(s[bb][r], c2, -m_use));
+        else e[r] = fast_exp2(s[bb][r] - m_use);
+        rs[r & 3] += e[r];
       }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const V8 pb = pack8<T>(e, 8 * c);
+        const char* vr = sV + (32 * bb + 16 * c) * C::ROWB;
+#pragma unroll
+        for (int db = 0; db < C::DB; ++db) {
+          const i16x4 lo = lds_read_tr4(vr + voff[db]);
+          const i16x4 hi = lds_read_tr4(vr + 8 * C::ROWB + voff[db]);
+          acc[db] = M::mma(cat_tr<V8>(lo, hi), pb, acc[db]);
+        }
+      }
+    }
+    l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+    // block 0's exps first, then each PV MFMA of block bb paired with
+    // transpose reads and a share of block bb+1's exp/convert VALU work
+    __builtin_amdgcn_sched_group_barrier(0x002, 24, 1);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+#pragma unroll
+    for (int i = 0; i < 2 * C::DB * C::NB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 1);
     }
   };
 
@@ -238,9 +276,7 @@ void fwd_mfma_kernel(FwdArgs a) {
     // window edge or the KV tail for some row of this wave.
     const bool need_mask = (n0 + C::BN > p.Skv) || (p.causal && n0 + C::BN - 1 > mw) ||
                            (p.window > 0 && mw + 31 - n0 > p.window);
-#pragma unroll
-    for (int bb = 0; bb < C::NB; ++bb)
-      block(n0 + 32 * bb, sK + 32 * bb * C::ROWB, sV + 32 * bb * C::ROWB, need_mask);
+    tile_body(sK, sV, n0, need_mask);
     st = st == 2 ? 0 : st + 1;
   }
 
