@@ -98,6 +98,15 @@ __device__ __forceinline__ void scale_inplace(f32x16& a, float s) {
   }
 }
 
+// Register fence: the value must be computed before this point and is read
+// again after it.  Volatile asm keeps its place relative to barriers, so this
+// stops the compiler from sinking a phase's results past a workgroup barrier
+// (or hoisting their consumers before it).
+template <class X>
+__device__ __forceinline__ void pin(X& x) {
+  asm volatile("" : "+v"(x));
+}
+
 // --- direct global -> LDS tile staging --------------------------------------
 // global_load_lds_dwordx4: lane l's 16 bytes land at LDS byte address
 // (lds_addr + 16 * l).  Issued through asm so that the compiler does not place
@@ -173,6 +182,50 @@ __device__ __forceinline__ typename Mfma<T>::v8 pack8(const f32x16& a, int o) {
 #pragma unroll
   for (int t = 0; t < 8; ++t) r[t] = from_f32<T>(a[o + t]);
   return r;
+}
+
+// max of two / three floats as single instructions.  fmaxf would first
+// quiet each operand (one extra instruction per input in IEEE mode); these
+// are only used where the inputs are scores, for which the NaN behaviour of
+// the plain instruction (a quiet NaN input is ignored) is acceptable.
+__device__ __forceinline__ float max2(float a, float b) {
+  float r;
+  asm("v_max_f32_e32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// Max of 16 accumulator values as 7 instructions, leaving two partials.
+__device__ __forceinline__ void max16_partial(const f32x16& s, float& f, float& g) {
+  const float a = max3(s[0], s[1], s[2]), b = max3(s[3], s[4], s[5]), c = max3(s[6], s[7], s[8]);
+  const float d = max3(s[9], s[10], s[11]), e = max3(s[12], s[13], s[14]);
+  f = max3(a, b, c);
+  g = max3(d, e, s[15]);
+}
+
+// acc + sum of the 8 16-bit values of an MFMA operand (fp32 accumulate).
+template <class T> struct Dot2;
+template <> struct Dot2<__bf16> {
+  typedef __bf16 x2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ float add(x2 a, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, x2{(__bf16)1.0f, (__bf16)1.0f}, c, false);
+  }
+};
+template <> struct Dot2<_Float16> {
+  typedef _Float16 x2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ float add(x2 a, float c) {
+    return __builtin_amdgcn_fdot2(a, x2{(_Float16)1.0f, (_Float16)1.0f}, c, false);
+  }
+};
+template <class T>
+__device__ __forceinline__ void sum8(typename Mfma<T>::v8 p, float (&acc)[4]) {
+  acc[0] = Dot2<T>::add(__builtin_shufflevector(p, p, 0, 1), acc[0]);
+  acc[1] = Dot2<T>::add(__builtin_shufflevector(p, p, 2, 3), acc[1]);
+  acc[2] = Dot2<T>::add(__builtin_shufflevector(p, p, 4, 5), acc[2]);
+  acc[3] = Dot2<T>::add(__builtin_shufflevector(p, p, 6, 7), acc[3]);
 }
 
 // Pack 4 fp32 values into 4 x T (8 bytes) for a store.

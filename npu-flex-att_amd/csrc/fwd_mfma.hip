@@ -51,7 +51,10 @@ struct FwdCfg {
   static constexpr int ROWB = D * 2;        // bytes per tile row
   static constexpr int TILEB = BN * ROWB;   // bytes per tile of one tensor
   static constexpr int E = TILEB / (1024 * NW);  // 1 KB loads per wave per tensor per tile
-  static constexpr int STAGES = 3;
+  // Ping-pong schedule (two waves per SIMD, one phase apart) when the
+  // workgroup has 8 waves; 4-wave workgroups (D = 256) run one wave per SIMD.
+  static constexpr bool PP = NW == 8;
+  static constexpr int STAGES = PP ? 4 : 3;
   static_assert(E >= 1 && E * 1024 * NW == TILEB, "tile must split into 1 KB loads per wave");
 };
 
@@ -261,23 +264,219 @@ void fwd_mfma_kernel(FwdArgs a) {
     }
   };
 
-  if (t_lo < t_hi) issue(t_lo, 0);
-  if (t_lo + 1 < t_hi) issue(t_lo + 1, 1);
-  int st = 0;
-  for (int t = t_lo; t < t_hi; ++t) {
-    if (t + 1 < t_hi) wait_vmcnt<2 * C::E>();
-    else wait_vmcnt<0>();
-    __syncthreads();
-    if (t + 2 < t_hi) issue(t + 2, st == 0 ? 2 : st - 1);
-    const char* sK = smem + st * 2 * C::TILEB;
-    const char* sV = sK + C::TILEB;
-    const int n0 = t * C::BN;
-    // Per element masking only on tiles that cut the causal diagonal, the
-    // window edge or the KV tail for some row of this wave.
-    const bool need_mask = (n0 + C::BN > p.Skv) || (p.causal && n0 + C::BN - 1 > mw) ||
-                           (p.window > 0 && mw + 31 - n0 > p.window);
-    tile_body(sK, sV, n0, need_mask);
-    st = st == 2 ? 0 : st + 1;
+  if constexpr (C::PP) {
+    // Ping-pong.  Waves 0-3 and 4-7 (one of each on every SIMD) run the same
+    // program one phase apart, phases separated by workgroup barriers:
+    //   MFMA phase  M(t): O^T += V^T P(t-1)^T and S^T(t) = K(t) Q^T, 32
+    //                     independent MFMAs fed from LDS;
+    //   VALU phase  V(t): mask, row max, rescale, P(t) = exp2(y - m), sums.
+    // While one wave of a SIMD is in its MFMA phase the other is in its VALU
+    // phase, so the matrix core is fed during the softmax.
+    // Tile u lives in stage (u - t_lo) % 4 from its copy (issued at the start
+    // of M(u-2)) until B's M(u+1) has read V(u); the copy of tile u+4 into
+    // that stage is issued at M(u+2), after the barrier that ends B's M(u+1).
+    const int grp = wave >> 2;
+    // Every M phase issues one tile copy: tile u into stage u % 4, with u
+    // clamped to the last tile (a redundant copy into a free stage), so that
+    // each wave always has exactly one copy in flight past the tile it
+    // needs next and every wait is vmcnt(2E) (vector memory operations
+    // complete in order, a tile is 2E of them per wave).
+    int64_t koffs[C::E], voffs[C::E];  // byte offsets of this lane's chunks within a tile
+    int krow[C::E];
+#pragma unroll
+    for (int e = 0; e < C::E; ++e) {
+      const int q = (wave * C::E + e) * 64 + lane;
+      const int row = q / C::CPR, pc = q % C::CPR;
+      krow[e] = row;
+      koffs[e] = ((int64_t)row * a.k.ss + swz_col<C::CPR>(row, pc) * 8) * (int64_t)sizeof(T);
+      voffs[e] = ((int64_t)row * a.v.ss + swz_tr_inv<C::CPR>(row, pc) * 8) * (int64_t)sizeof(T);
+    }
+    auto issue_pp = [&](int t) {
+      const int st = (t - t_lo) & 3;
+      const int n0 = min(t, t_hi - 1) * C::BN;
+      const unsigned sbase = lds0 + st * 2 * C::TILEB;
+      if (n0 + C::BN <= p.Skv) {
+        const char* kb = (const char*)(kp + (int64_t)n0 * a.k.ss);
+        const char* vb = (const char*)(vp + (int64_t)n0 * a.v.ss);
+#pragma unroll
+        for (int e = 0; e < C::E; ++e) {
+          const unsigned dst = sbase + (wave * C::E + e) * 1024;
+          load_lds16(kb + koffs[e], dst);
+          load_lds16(vb + voffs[e], dst + C::TILEB);
+        }
+      } else {
+        issue(min(t, t_hi - 1), st);  // KV tail: rows clamped to Skv - 1
+      }
+    };
+    auto wait_tile = [&]() { wait_vmcnt<2 * C::E>(); };
+    f32x16 s[C::NB];
+    V8 P[2 * C::NB];
+
+    auto softmax = [&](int n0) {
+      if constexpr (!RAW) {
+#pragma unroll
+        for (int bb = 0; bb < C::NB; ++bb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
+            float tv;
+            s[bb][r] = score_log2<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2, my_m, j, tv);
+          }
+      }
+      const bool need_mask = (n0 + C::BN > p.Skv) || (p.causal && n0 + C::BN - 1 > mw) ||
+                             (p.window > 0 && mw + 31 - n0 > p.window);
+      if (need_mask) {
+#pragma unroll
+        for (int bb = 0; bb < C::NB; ++bb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (!allowed(p, my_m, j)) s[bb][r] = kNegInf;
+          }
+          pin(s[bb]);  // finished inside the branch (no selects after it)
+        }
+      }
+      float mp[2 * C::NB];
+#pragma unroll
+      for (int bb = 0; bb < C::NB; ++bb) max16_partial(s[bb], mp[2 * bb], mp[2 * bb + 1]);
+      float mx;
+      if constexpr (C::NB == 1) mx = max2(mp[0], mp[1]);
+      else if constexpr (C::NB == 2) mx = max2(max3(mp[0], mp[1], mp[2]), mp[3]);
+      else {
+        float u = max3(mp[0], mp[1], mp[2]);
+        u = max3(u, mp[3], mp[4]);
+        u = max3(u, mp[5], mp[6]);
+        mx = max2(u, mp[7]);
+      }
+      if constexpr (RAW) mx *= c2;
+      mx = fmaxf(mx, swap_halves(mx));
+      if (mx != mx) mx = kNegInf;
+      const bool grow = mx > m_run + kRescaleThreshold;
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float m_new = grow ? mx : m_run;
+        const float alpha = grow ? fast_exp2(m_run - m_new) : 1.f;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < C::DB; ++db) scale_inplace(acc[db], alpha);
+        m_run = m_new;
+      }
+      const float m_use = (m_run == kNegInf) ? 0.f : m_run;
+#pragma unroll
+      for (int bb = 0; bb < C::NB; ++bb) {
+        f32x16 e;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          if constexpr (RAW) e[r] = fast_exp2(__builtin_fmaf(s[bb][r], c2, -m_use));
+          else e[r] = fast_exp2(s[bb][r] - m_use);
+        }
+        P[2 * bb] = pack8<T>(e, 0);
+        P[2 * bb + 1] = pack8<T>(e, 8);
+      }
+      // row sums of the rounded P (the values the PV MFMAs consume)
+      float rs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 2 * C::NB; ++i) sum8<T>(P[i], rs);
+      l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+#pragma unroll
+      for (int i = 0; i < 2 * C::NB; ++i) pin(P[i]);  // P done before the barrier
+      pin(l_run);
+    };
+    // scores read only after the barrier that ends their MFMA phase
+    auto pin_s = [&]() {
+#pragma unroll
+      for (int bb = 0; bb < C::NB; ++bb) pin(s[bb]);
+    };
+
+    // MFMA phase: PV of the previous tile (stage sv) and/or S^T of the next
+    // (stage sk), interleaved so that the two accumulator sets never wait on
+    // each other; LDS reads are kept two MFMA pairs ahead.
+    constexpr int NPV = 2 * C::NB * C::DB;  // == NB * KC
+    auto mphase = [&](int sv, int sk, bool do_pv, bool do_s) {
+      const char* sV = smem + sv * 2 * C::TILEB + C::TILEB;
+      const char* sK = smem + sk * 2 * C::TILEB;
+#ifdef FLEXATT_FWD_SETPRIO
+      __builtin_amdgcn_s_setprio(1);
+#endif
+      if (do_s) {
+#pragma unroll
+        for (int bb = 0; bb < C::NB; ++bb) s[bb] = f32x16{};
+      }
+#pragma unroll
+      for (int i = 0; i < NPV; ++i) {
+        if (do_pv) {
+          const int db = i % C::DB, c = (i / C::DB) & 1, bb = i / (2 * C::DB);
+          const char* vr = sV + (32 * bb + 16 * c) * C::ROWB + voff[db];
+          const i16x4 lo = lds_read_tr4(vr);
+          const i16x4 hi = lds_read_tr4(vr + 8 * C::ROWB);
+          acc[db] = M::mma(cat_tr<V8>(lo, hi), P[2 * bb + c], acc[db]);
+        }
+        if (do_s) {
+          const int bb = i % C::NB, kc = i / C::NB;
+          s[bb] = M::mma(as_v8<V8>(lds_read16(sK + bb * 32 * C::ROWB + koff[kc])), qf[kc], s[bb]);
+        }
+      }
+      if (do_pv && do_s) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 2);
+#pragma unroll
+        for (int i = 0; i < NPV - 2; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 2);
+          __builtin_amdgcn_sched_group_barrier(0x100, 3, 2);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
+      }
+#ifdef FLEXATT_FWD_SETPRIO
+      __builtin_amdgcn_s_setprio(0);
+#endif
+    };
+
+    if (t_lo < t_hi) {
+      issue_pp(t_lo);
+      issue_pp(t_lo + 1);
+      wait_tile();
+      __syncthreads();
+      if (grp) __syncthreads();  // second half starts one phase late
+      issue_pp(t_lo + 2);
+      mphase(0, 0, false, true);
+      wait_tile();
+      __syncthreads();
+      pin_s();
+      for (int t = t_lo; t + 1 < t_hi; ++t) {
+        softmax(t * C::BN);
+        wait_tile();
+        __syncthreads();
+        issue_pp(t + 3);
+        mphase((t - t_lo) & 3, (t + 1 - t_lo) & 3, true, true);
+        wait_tile();
+        __syncthreads();
+        pin_s();
+      }
+      softmax((t_hi - 1) * C::BN);
+      wait_tile();
+      __syncthreads();
+      mphase((t_hi - 1 - t_lo) & 3, 0, true, false);
+      wait_vmcnt<0>();  // no copy may land after the workgroup's LDS is released
+      __syncthreads();
+      if (!grp) __syncthreads();  // first half: match the second's count
+    }
+  } else {
+    if (t_lo < t_hi) issue(t_lo, 0);
+    if (t_lo + 1 < t_hi) issue(t_lo + 1, 1);
+    int st = 0;
+    for (int t = t_lo; t < t_hi; ++t) {
+      if (t + 1 < t_hi) wait_vmcnt<2 * C::E>();
+      else wait_vmcnt<0>();
+      __syncthreads();
+      if (t + 2 < t_hi) issue(t + 2, st == 0 ? 2 : st - 1);
+      const char* sK = smem + st * 2 * C::TILEB;
+      const char* sV = sK + C::TILEB;
+      const int n0 = t * C::BN;
+      // Per element masking only on tiles that cut the causal diagonal, the
+      // window edge or the KV tail for some row of this wave.
+      const bool need_mask = (n0 + C::BN > p.Skv) || (p.causal && n0 + C::BN - 1 > mw) ||
+                             (p.window > 0 && mw + 31 - n0 > p.window);
+      tile_body(sK, sV, n0, need_mask);
+      st = st == 2 ? 0 : st + 1;
+    }
   }
 
   const float l_tot = l_run + swap_halves(l_run);
