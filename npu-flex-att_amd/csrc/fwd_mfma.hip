@@ -55,6 +55,11 @@ struct FwdCfg {
   // workgroup has 8 waves; 4-wave workgroups (D = 256) run one wave per SIMD.
   static constexpr bool PP = NW == 8;
   static constexpr int STAGES = PP ? 4 : 3;
+#ifdef FLEXATT_FWD_PF
+  static constexpr int PF = FLEXATT_FWD_PF;  // tuning override
+#else
+  static constexpr int PF = 2;  // MFMA pairs whose LDS reads are issued ahead
+#endif
   static_assert(E >= 1 && E * 1024 * NW == TILEB, "tile must split into 1 KB loads per wave");
 };
 
@@ -267,51 +272,64 @@ void fwd_mfma_kernel(FwdArgs a) {
   if constexpr (C::PP) {
     // Ping-pong.  Waves 0-3 and 4-7 (one of each on every SIMD) run the same
     // program one phase apart, phases separated by workgroup barriers:
-    //   MFMA phase  M(t): O^T += V^T P(t-1)^T and S^T(t) = K(t) Q^T, 32
-    //                     independent MFMAs fed from LDS;
-    //   VALU phase  V(t): mask, row max, rescale, P(t) = exp2(y - m), sums.
+    //   MFMA phase  M(t): S^T(t) = K(t) Q^T and O^T += V^T P(t-1)^T, 32
+    //                     independent MFMAs fed from LDS, with the packing of
+    //                     P(t-1) and its row sums issued in their shadow;
+    //   VALU phase  V(t): mask, row max, rescale, E(t) = exp2(y - m).
     // While one wave of a SIMD is in its MFMA phase the other is in its VALU
-    // phase, so the matrix core is fed during the softmax.
+    // phase.  A single wave issues VALU work at well under the SIMD's VALU
+    // rate, so both waves carry part of the softmax work.
     // Tile u lives in stage (u - t_lo) % 4 from its copy (issued at the start
     // of M(u-2)) until B's M(u+1) has read V(u); the copy of tile u+4 into
     // that stage is issued at M(u+2), after the barrier that ends B's M(u+1).
     const int grp = wave >> 2;
-    // Every M phase issues one tile copy: tile u into stage u % 4, with u
-    // clamped to the last tile (a redundant copy into a free stage), so that
-    // each wave always has exactly one copy in flight past the tile it
-    // needs next and every wait is vmcnt(2E) (vector memory operations
-    // complete in order, a tile is 2E of them per wave).
+    // Tile copies are issued in tile order, one per M phase, past the last
+    // tile as redundant copies of it into a free stage, so that each wave
+    // always has exactly one copy in flight beyond the tile it needs next and
+    // every wait is vmcnt(2E) (vector memory operations complete in order, a
+    // tile is 2E of them per wave).
     int64_t koffs[C::E], voffs[C::E];  // byte offsets of this lane's chunks within a tile
-    int krow[C::E];
 #pragma unroll
     for (int e = 0; e < C::E; ++e) {
       const int q = (wave * C::E + e) * 64 + lane;
       const int row = q / C::CPR, pc = q % C::CPR;
-      krow[e] = row;
       koffs[e] = ((int64_t)row * a.k.ss + swz_col<C::CPR>(row, pc) * 8) * (int64_t)sizeof(T);
       voffs[e] = ((int64_t)row * a.v.ss + swz_tr_inv<C::CPR>(row, pc) * 8) * (int64_t)sizeof(T);
     }
-    auto issue_pp = [&](int t) {
+    const int64_t kstep = (int64_t)C::BN * a.k.ss * (int64_t)sizeof(T);
+    const int64_t vstep = (int64_t)C::BN * a.v.ss * (int64_t)sizeof(T);
+    const char* kcur = (const char*)(kp + (int64_t)t_lo * C::BN * a.k.ss);
+    const char* vcur = (const char*)(vp + (int64_t)t_lo * C::BN * a.v.ss);
+    int next_t = t_lo;
+    auto issue_next = [&]() {
+      const int t = next_t++;
       const int st = (t - t_lo) & 3;
-      const int n0 = min(t, t_hi - 1) * C::BN;
-      const unsigned sbase = lds0 + st * 2 * C::TILEB;
-      if (n0 + C::BN <= p.Skv) {
-        const char* kb = (const char*)(kp + (int64_t)n0 * a.k.ss);
-        const char* vb = (const char*)(vp + (int64_t)n0 * a.v.ss);
+      if (t < t_hi && (t + 1) * C::BN <= p.Skv) {
+        const unsigned dst = lds0 + st * 2 * C::TILEB + wave * C::E * 1024;
 #pragma unroll
         for (int e = 0; e < C::E; ++e) {
-          const unsigned dst = sbase + (wave * C::E + e) * 1024;
-          load_lds16(kb + koffs[e], dst);
-          load_lds16(vb + voffs[e], dst + C::TILEB);
+          load_lds16(kcur + koffs[e], dst + e * 1024);
+          load_lds16(vcur + voffs[e], dst + e * 1024 + C::TILEB);
         }
+        kcur += kstep;
+        vcur += vstep;
       } else {
-        issue(min(t, t_hi - 1), st);  // KV tail: rows clamped to Skv - 1
+        issue(min(t, t_hi - 1), st);  // KV tail (rows clamped to Skv - 1) or redundant copy
       }
     };
     auto wait_tile = [&]() { wait_vmcnt<2 * C::E>(); };
-    f32x16 s[C::NB];
-    V8 P[2 * C::NB];
+    f32x16 s[C::NB];  // scores of the tile in flight
+    V8 P[2 * C::NB];  // exp2(y - m) of the previous tile as the PV MFMA operand
 
+    // Tiles [tm_lo, tm_hi) are fully allowed for every row of this wave:
+    // below tm_lo a row may be outside the window, from tm_hi on a tile may
+    // cross the causal diagonal or the KV tail.
+    int tm_hi = p.Skv / C::BN;  // tiles wholly inside the KV length
+    if (p.causal) tm_hi = min(tm_hi, (mw + 1) / C::BN);  // n0 + BN - 1 <= mw
+    int tm_lo = 0;
+    if (p.window > 0) tm_lo = max(0, (mw + 31 - p.window + C::BN - 1) / C::BN);  // mw + 31 - n0 <= window
+    tm_hi = __builtin_amdgcn_readfirstlane(tm_hi);
+    tm_lo = __builtin_amdgcn_readfirstlane(tm_lo);
     auto softmax = [&](int n0) {
       if constexpr (!RAW) {
 #pragma unroll
@@ -323,9 +341,8 @@ void fwd_mfma_kernel(FwdArgs a) {
             s[bb][r] = score_log2<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2, my_m, j, tv);
           }
       }
-      const bool need_mask = (n0 + C::BN > p.Skv) || (p.causal && n0 + C::BN - 1 > mw) ||
-                             (p.window > 0 && mw + 31 - n0 > p.window);
-      if (need_mask) {
+      const int tn = n0 / C::BN;
+      if (tn < tm_lo || tn >= tm_hi) {
 #pragma unroll
         for (int bb = 0; bb < C::NB; ++bb) {
 #pragma unroll
@@ -361,6 +378,9 @@ void fwd_mfma_kernel(FwdArgs a) {
         m_run = m_new;
       }
       const float m_use = (m_run == kNegInf) ? 0.f : m_run;
+      // (fp32 adds for the row sums: dot2 instructions share the matrix pipe
+      // and would stall behind the other wave's MFMAs)
+      float rs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int bb = 0; bb < C::NB; ++bb) {
         f32x16 e;
@@ -368,35 +388,34 @@ void fwd_mfma_kernel(FwdArgs a) {
         for (int r = 0; r < 16; ++r) {
           if constexpr (RAW) e[r] = fast_exp2(__builtin_fmaf(s[bb][r], c2, -m_use));
           else e[r] = fast_exp2(s[bb][r] - m_use);
+          rs[r & 3] += e[r];
         }
         P[2 * bb] = pack8<T>(e, 0);
         P[2 * bb + 1] = pack8<T>(e, 8);
       }
-      // row sums of the rounded P (the values the PV MFMAs consume)
-      float rs[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < 2 * C::NB; ++i) sum8<T>(P[i], rs);
       l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+      // done before the barrier
 #pragma unroll
-      for (int i = 0; i < 2 * C::NB; ++i) pin(P[i]);  // P done before the barrier
+      for (int i = 0; i < 2 * C::NB; ++i) pin(P[i]);
       pin(l_run);
     };
-    // scores read only after the barrier that ends their MFMA phase
+    // phase inputs are read only after the barrier that ends their producer
     auto pin_s = [&]() {
 #pragma unroll
       for (int bb = 0; bb < C::NB; ++bb) pin(s[bb]);
     };
+    auto pin_p = [&]() {
+#pragma unroll
+      for (int i = 0; i < 2 * C::NB; ++i) pin(P[i]);
+    };
 
     // MFMA phase: PV of the previous tile (stage sv) and/or S^T of the next
     // (stage sk), interleaved so that the two accumulator sets never wait on
-    // each other; LDS reads are kept two MFMA pairs ahead.
+    // each other; LDS reads are kept PF MFMA pairs ahead.
     constexpr int NPV = 2 * C::NB * C::DB;  // == NB * KC
     auto mphase = [&](int sv, int sk, bool do_pv, bool do_s) {
       const char* sV = smem + sv * 2 * C::TILEB + C::TILEB;
       const char* sK = smem + sk * 2 * C::TILEB;
-#ifdef FLEXATT_FWD_SETPRIO
-      __builtin_amdgcn_s_setprio(1);
-#endif
       if (do_s) {
 #pragma unroll
         for (int bb = 0; bb < C::NB; ++bb) s[bb] = f32x16{};
@@ -416,26 +435,23 @@ void fwd_mfma_kernel(FwdArgs a) {
         }
       }
       if (do_pv && do_s) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 6, 2);
+        __builtin_amdgcn_sched_group_barrier(0x100, 3 * C::PF, 2);
 #pragma unroll
-        for (int i = 0; i < NPV - 2; ++i) {
+        for (int i = 0; i < NPV - C::PF; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 2, 2);
           __builtin_amdgcn_sched_group_barrier(0x100, 3, 2);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * C::PF, 2);
       }
-#ifdef FLEXATT_FWD_SETPRIO
-      __builtin_amdgcn_s_setprio(0);
-#endif
     };
 
     if (t_lo < t_hi) {
-      issue_pp(t_lo);
-      issue_pp(t_lo + 1);
+      issue_next();  // t_lo
+      issue_next();  // t_lo + 1
       wait_tile();
       __syncthreads();
       if (grp) __syncthreads();  // second half starts one phase late
-      issue_pp(t_lo + 2);
+      issue_next();  // t_lo + 2
       mphase(0, 0, false, true);
       wait_tile();
       __syncthreads();
@@ -444,7 +460,8 @@ void fwd_mfma_kernel(FwdArgs a) {
         softmax(t * C::BN);
         wait_tile();
         __syncthreads();
-        issue_pp(t + 3);
+        pin_p();
+        issue_next();  // t + 3
         mphase((t - t_lo) & 3, (t + 1 - t_lo) & 3, true, true);
         wait_tile();
         __syncthreads();
@@ -453,6 +470,7 @@ void fwd_mfma_kernel(FwdArgs a) {
       softmax((t_hi - 1) * C::BN);
       wait_tile();
       __syncthreads();
+      pin_p();
       mphase((t_hi - 1 - t_lo) & 3, 0, true, false);
       wait_vmcnt<0>();  // no copy may land after the workgroup's LDS is released
       __syncthreads();
