@@ -10,7 +10,12 @@ bwd = 2.5 * fwd (recomputation not counted).  Peak = 2516.6 TFLOP/s
 (256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU).
 
 Prints ONE JSON line.  Per-kernel times come from HIP events recorded on the
-stream the kernels are launched on (torch's current stream).
+stream the kernels are launched on (torch's current stream).  The roofline
+"traffic" field (HBM bytes per launch of the dominant kernel) cannot be read
+from inside the process: it is the figure recorded by the two rocprofv3
+counter passes (FETCH_SIZE, WRITE_SIZE, calibrated on a plain device copy)
+over this same command, kept in profiles/hbm_traffic_<config>.md, and null
+when no such record exists for the workload.
 """
 import argparse
 import json
@@ -46,6 +51,27 @@ def parse():
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one 256 MiB device copy (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+def recorded_traffic(config, kernel):
+    """HBM bytes per dispatch of `kernel` from profiles/hbm_traffic_<config>.md."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{config}.md")
+    try:
+        lines = open(path).read().splitlines()
+    except OSError:
+        return None
+    header = None
+    for line in lines:
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if header is None and "HBM bytes" in cells:
+            header = cells
+            continue
+        if header and cells and cells[0] == kernel:
+            try:
+                return int(cells[header.index("HBM bytes")])
+            except (ValueError, IndexError):
+                return None
+    return None
 
 
 def pairs(sq, skv, causal, window):
@@ -192,7 +218,7 @@ def main():
             "peak": PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": recorded_traffic(args.config, dom),
         },
         "cpu_baseline": cpu,
     }
