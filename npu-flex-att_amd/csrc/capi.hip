@@ -89,8 +89,8 @@ const BwdLauncher kDq[3][4] = {
 };
 const BwdLauncher kDkdv[3][4] = {
     {bwd_dkdv_simt_f32_d32, bwd_dkdv_simt_f32_d64, bwd_dkdv_simt_f32_d128, bwd_dkdv_simt_f32_d256},
-    {bwd_dkdv_mfma_f16_d32, bwd_dkdv_mfma_f16_d64, bwd_dkdv_mfma_f16_d128, bwd_dkdv_mfma_f16_d256},
-    {bwd_dkdv_mfma_bf16_d32, bwd_dkdv_mfma_bf16_d64, bwd_dkdv_mfma_bf16_d128, bwd_dkdv_mfma_bf16_d256},
+    {bwd_dkdv_mfma_f16_d32, bwd_dkdv_mfma_f16_d64, bwd_kv_f16_d128, bwd_dkdv_mfma_f16_d256},
+    {bwd_dkdv_mfma_bf16_d32, bwd_dkdv_mfma_bf16_d64, bwd_kv_bf16_d128, bwd_dkdv_mfma_bf16_d256},
 };
 
 #define FLEXATT_TRY(x)             \

@@ -117,6 +117,10 @@ __device__ __forceinline__ void pin(X& x) {
 __device__ __forceinline__ void load_lds16(const void* gptr, unsigned lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr) : "memory");
 }
+// Same for one dword per lane (lane l's 4 bytes land at lds_addr + 4 * l).
+__device__ __forceinline__ void load_lds4(const void* gptr, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(gptr), "s"(lds_addr) : "memory");
+}
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -147,6 +151,22 @@ __device__ __forceinline__ int swz_tr_inv(int r, int p) {
   if constexpr (CPR == 4) return p;
   else if constexpr (CPR == 8) return (p - 4 * ((r >> 1) & 1)) & 7;
   else return (p - 4 * r) & (CPR - 1);
+}
+
+// One layout for tiles that are read both ways: 16-byte column reads (rows
+// as MFMA A operands) and transpose reads (columns as A operands).  Chunk c
+// of row r sits at chunk (c + 2r + bit3(r)) mod CPR: conflict-free for both
+// patterns (measured 255 B/clk/CU for the b128 reads and 126 B/clk/CU for the
+// transpose reads, each the LDS peak for that width).
+template <int CPR>
+__device__ __forceinline__ int swz_dual(int r, int c) {
+  static_assert(CPR == 16, "dual-use swizzle is defined for 256-byte rows");
+  return (c + 2 * r + ((r >> 3) & 1)) & (CPR - 1);
+}
+template <int CPR>
+__device__ __forceinline__ int swz_dual_inv(int r, int p) {
+  static_assert(CPR == 16, "dual-use swizzle is defined for 256-byte rows");
+  return (p - 2 * r - ((r >> 3) & 1)) & (CPR - 1);
 }
 
 // Value of lane l ^ 32 (the other half of the wave).

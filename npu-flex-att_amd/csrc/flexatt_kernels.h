@@ -52,4 +52,8 @@ FLEXATT_DECL_D(256)
 
 hipError_t bwd_delta(int dtype, const DeltaArgs&, hipStream_t);
 
+// dK/dV as a KV-stationary tile stream (bwd_kv.hip), D = 128.
+hipError_t bwd_kv_bf16_d128(const BwdArgs&, hipStream_t);
+hipError_t bwd_kv_f16_d128(const BwdArgs&, hipStream_t);
+
 }  // namespace flexatt
