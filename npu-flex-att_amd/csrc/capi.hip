@@ -84,8 +84,8 @@ const FwdLauncher kFwd[3][4] = {
 };
 const BwdLauncher kDq[3][4] = {
     {bwd_dq_simt_f32_d32, bwd_dq_simt_f32_d64, bwd_dq_simt_f32_d128, bwd_dq_simt_f32_d256},
-    {bwd_dq_mfma_f16_d32, bwd_dq_mfma_f16_d64, bwd_dq_mfma_f16_d128, bwd_dq_mfma_f16_d256},
-    {bwd_dq_mfma_bf16_d32, bwd_dq_mfma_bf16_d64, bwd_dq_mfma_bf16_d128, bwd_dq_mfma_bf16_d256},
+    {bwd_dq_mfma_f16_d32, bwd_dq_mfma_f16_d64, bwd_q_f16_d128, bwd_dq_mfma_f16_d256},
+    {bwd_dq_mfma_bf16_d32, bwd_dq_mfma_bf16_d64, bwd_q_bf16_d128, bwd_dq_mfma_bf16_d256},
 };
 const BwdLauncher kDkdv[3][4] = {
     {bwd_dkdv_simt_f32_d32, bwd_dkdv_simt_f32_d64, bwd_dkdv_simt_f32_d128, bwd_dkdv_simt_f32_d256},

@@ -56,4 +56,8 @@ hipError_t bwd_delta(int dtype, const DeltaArgs&, hipStream_t);
 hipError_t bwd_kv_bf16_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_f16_d128(const BwdArgs&, hipStream_t);
 
+// dQ as a query-stationary tile stream (bwd_q.hip), D = 128.
+hipError_t bwd_q_bf16_d128(const BwdArgs&, hipStream_t);
+hipError_t bwd_q_f16_d128(const BwdArgs&, hipStream_t);
+
 }  // namespace flexatt
