@@ -55,7 +55,7 @@ struct KvCfg {
   static constexpr int TILEB = BM * ROWB;              // one of Q / dO
   static constexpr int E = TILEB / (1024 * NW);        // 1 KB copies per wave per tensor
   static constexpr int STAGEB = 2 * TILEB + 2 * BM * 4;  // Q, dO, LSE, Delta
-  static constexpr int STAGES = 4;
+  static constexpr int STAGES = 8;                     // copies run four tiles ahead
   static constexpr int NPK = 2 * QB;                   // packed P (or dS) operands per tile
   static_assert(E * 1024 * NW == TILEB, "tile must split into 1 KB copies");
   static constexpr int RPW = BM / NW;                  // LSE / Delta values copied per wave
@@ -115,7 +115,7 @@ void bwd_kv_kernel(BwdArgs a) {
     dv[db] = f32x16{};
   }
 
-  // Tile copies: tile u -> stage u % 4; past the end, redundant copies of the
+  // Tile copies: tile u -> stage u % 8; past the end, redundant copies of the
   // last tile into a free stage keep every wave at 2E + 2 operations per tile.
   const unsigned lds0 = lds_addr_of(smem);
   int crow[C::E], cchk[C::E];  // row / logical chunk of this lane in copy e
@@ -125,31 +125,74 @@ void bwd_kv_kernel(BwdArgs a) {
     crow[e] = q / C::CPR;
     cchk[e] = swz_dual_inv<C::CPR>(crow[e], q % C::CPR);
   }
-  int is_g = 0, is_qt = qt_lo;  // next tile to copy (head, query tile)
-  auto issue = [&](int u) {
-    const unsigned sb = lds0 + (u & 3) * C::STAGEB;
-    const int hq = hk * p.G + min(is_g, p.G - 1);
-    const int m0 = (is_g < p.G ? is_qt : qt_lo + nqt - 1) * C::BM;
-    const T* qg = (const T*)a.q.data + b * a.q.sb + hq * a.q.sh;
-    const T* og = (const T*)a.dout.data + b * a.dout.sb + hq * a.dout.sh;
+  // Copies of one tile: E Q rows chunks, E dO chunks and one load of 8 LSE
+  // plus 8 Delta values per wave (lanes 0-7 / 8-15), i.e. 2E + 1 operations
+  // per wave.  Per tile only scalar bases move; the per-lane offsets are
+  // recomputed (clamped to row Sq - 1) only for a query-tail tile.
+  const int rl = 8 * wave + (lane & 7);  // LSE / Delta row of this lane's copy
+  int64_t cq[C::E], co[C::E];            // per-lane byte offsets, current tile
+  int crl;                               // row of the LSE / Delta copy, current tile
+  auto set_offsets = [&](int last) {     // last = Sq - 1 - m0 (clamp)
 #pragma unroll
     for (int e = 0; e < C::E; ++e) {
-      const int64_t r = min(m0 + crow[e], p.Sq - 1);
-      const unsigned dst = sb + (wave * C::E + e) * 1024;
-      load_lds16(qg + r * a.q.ss + cchk[e] * 8, dst);
-      load_lds16(og + r * a.dout.ss + cchk[e] * 8, dst + C::TILEB);
+      const int64_t r = min(crow[e], last);
+      cq[e] = (r * a.q.ss + cchk[e] * 8) * (int64_t)sizeof(T);
+      co[e] = (r * a.dout.ss + cchk[e] * 8) * (int64_t)sizeof(T);
     }
-    const int64_t rr = (int64_t)(b * p.Hq + hq) * p.Sq + min(m0 + C::RPW * wave + lane, p.Sq - 1);
-    if (lane < C::RPW) {
-      load_lds4(a.lse + rr, sb + 2 * C::TILEB + 4 * C::RPW * wave);
-      load_lds4(a.delta + rr, sb + 2 * C::TILEB + C::BM * 4 + 4 * C::RPW * wave);
-    }
-    if (++is_qt == qt_lo + nqt) {
-      is_qt = qt_lo;
-      ++is_g;
+    crl = min(rl, last);
+  };
+  const int64_t qstep = (int64_t)C::BM * a.q.ss * (int64_t)sizeof(T);
+  const int64_t ostep = (int64_t)C::BM * a.dout.ss * (int64_t)sizeof(T);
+  int is_g = 0, is_qt = qt_lo;  // next tile to copy (head, query tile)
+  const char *qcur, *ocur;      // its Q / dO row m0
+  const float* lcur;            // its LSE (lanes 0-7) or Delta (lanes 8-15) row m0
+  bool tail = false;            // offsets currently clamped
+  auto set_head = [&](int g) {
+    const int hq = hk * p.G + g;
+    const int64_t m0 = (int64_t)qt_lo * C::BM;
+    qcur = (const char*)((const T*)a.q.data + b * a.q.sb + hq * a.q.sh + m0 * a.q.ss);
+    ocur = (const char*)((const T*)a.dout.data + b * a.dout.sb + hq * a.dout.sh + m0 * a.dout.ss);
+    lcur = (lane < 8 ? a.lse : a.delta) + (int64_t)(b * p.Hq + hq) * p.Sq + m0;
+  };
+  auto prep = [&]() {  // offsets for the tile (is_g, is_qt)
+    const int m0 = is_qt * C::BM;
+    const bool t = m0 + C::BM > p.Sq;
+    if (t || tail) set_offsets(t ? p.Sq - 1 - m0 : C::BM);
+    tail = t;
+  };
+  set_head(0);
+  set_offsets(C::BM);
+  prep();
+  // Copy operation j (0 .. 2E) of the tile going to stage u % 8.
+  auto copy_op = [&](int u, int j) {
+    const unsigned sb = lds0 + (u & 7) * C::STAGEB;
+    if (j < C::E) {
+      load_lds16(qcur + cq[j], sb + (wave * C::E + j) * 1024);
+    } else if (j < 2 * C::E) {
+      load_lds16(ocur + co[j - C::E], sb + C::TILEB + (wave * C::E + j - C::E) * 1024);
+    } else if (lane < 16) {
+      load_lds4(lcur + crl, sb + 2 * C::TILEB + 64 * wave);
     }
   };
-  auto wait_tile = [&]() { wait_vmcnt<2 * C::E + 2>(); };
+  // Move to the next tile to copy (past the end the last tile is copied again).
+  auto advance = [&]() {
+    if (is_g < p.G - 1 || is_qt < qt_lo + nqt - 1) {
+      if (++is_qt == qt_lo + nqt) {
+        is_qt = qt_lo;
+        set_head(++is_g);
+      } else {
+        qcur += qstep;
+        ocur += ostep;
+        lcur += C::BM;
+      }
+      prep();
+    }
+  };
+  auto issue = [&](int u) {
+#pragma unroll
+    for (int j = 0; j <= 2 * C::E; ++j) copy_op(u, j);
+    advance();
+  };
 
   // Lane-constant LDS byte offsets.
   int koff[C::KC], voff_lo[C::DB], voff_hi[C::DB];
@@ -169,105 +212,25 @@ void bwd_kv_kernel(BwdArgs a) {
   constexpr bool RAW = !SOFTCAP && !ALIBI;
   const float c2 = p.scale_log2;
 
-  f32x16 S[C::QB], DP[C::QB];  // scores and dP of the tile being processed
-  V8 PP[C::NPK], PS[C::NPK];    // packed P and dS of the previous tile
-
-  // S = Q K^T and dP = dO V^T of the tile in stage st (lane = KV row).
-  auto mma_s = [&](int st) {
-    const char* sQ = smem + st * C::STAGEB;
-    const char* sO = sQ + C::TILEB;
-#pragma unroll
-    for (int qb = 0; qb < C::QB; ++qb) {
-      S[qb] = f32x16{};
-      DP[qb] = f32x16{};
-    }
-#pragma unroll
-    for (int kc = 0; kc < C::KC; ++kc) {
-#pragma unroll
-      for (int qb = 0; qb < C::QB; ++qb)
-        S[qb] = M::mma(as_v8<V8>(lds_read16(sQ + qb * 32 * C::ROWB + koff[kc])), kreg[kc], S[qb]);
-#pragma unroll
-      for (int qb = 0; qb < C::QB; ++qb)
-        DP[qb] = M::mma(as_v8<V8>(lds_read16(sO + qb * 32 * C::ROWB + koff[kc])), vreg[kc], DP[qb]);
-    }
+  // Two register sets alternate between pipeline iterations (no copies):
+  // iteration u reads S / dP of tile u and packed P / dS of tile u-1 from its
+  // current set, and writes S / dP of tile u+1 and P / dS of tile u to the
+  // other set.
+  struct Set {
+    f32x16 S, DP;
+    V8 PP[C::NPK], PS[C::NPK];
   };
+  Set s0, s1;
 
-  // dV^T += dO^T P and dK^T += Q^T dS for the tile in stage st.
-  auto mma_kv = [&](int st) {
-    const char* sQ = smem + st * C::STAGEB;
-    const char* sO = sQ + C::TILEB;
-#pragma unroll
-    for (int qb = 0; qb < C::QB; ++qb)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int rb = (32 * qb + 16 * c) * C::ROWB;
-#pragma unroll
-        for (int db = 0; db < C::DB; ++db) {
-          const i16x4 olo = lds_read_tr4(sO + rb + voff_lo[db]);
-          const i16x4 ohi = lds_read_tr4(sO + rb + voff_hi[db]);
-          dv[db] = M::mma(cat_tr<V8>(olo, ohi), PP[2 * qb + c], dv[db]);
-          const i16x4 qlo = lds_read_tr4(sQ + rb + voff_lo[db]);
-          const i16x4 qhi = lds_read_tr4(sQ + rb + voff_hi[db]);
-          dk[db] = M::mma(cat_tr<V8>(qlo, qhi), PS[2 * qb + c], dk[db]);
-        }
-      }
-  };
-
-  // LSE and Delta of this lane's 4 * QB * 4 query rows of the tile in stage st.
-  f32x4 L4[C::QB * 4], D4[C::QB * 4];
+  // LSE and Delta of this lane's 16 query rows of the tile in stage st
+  // (stored per 8 rows: 8 LSE values, then 8 Delta values).
+  f32x4 L4[4], D4[4];
   auto read_rows = [&](int st) {
-    const float* sL = (const float*)(smem + st * C::STAGEB + 2 * C::TILEB);
-    const float* sD = sL + C::BM;
+    const float* sR = (const float*)(smem + st * C::STAGEB + 2 * C::TILEB);
 #pragma unroll
-    for (int qb = 0; qb < C::QB; ++qb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ro = 32 * qb + 8 * i + 4 * h;
-        L4[4 * qb + i] = __builtin_bit_cast(f32x4, lds_read16(sL + ro));
-        D4[4 * qb + i] = __builtin_bit_cast(f32x4, lds_read16(sD + ro));
-      }
-  };
-
-  // P and dS of the current tile (query rows m0.., LSE / Delta in L4 / D4)
-  // from S / DP.  MASKED: per-element mask, query tail, and exact zeros for
-  // masked pairs.
-  auto valu = [&](int m0, float slope_log2, bool masked, V8 (&pp)[C::NPK], V8 (&ps)[C::NPK]) {
-#pragma unroll
-    for (int qb = 0; qb < C::QB; ++qb) {
-      f32x16 pe, de;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ro = 32 * qb + 8 * i + 4 * h;
-        const f32x4 l4 = L4[4 * qb + i];
-        const f32x4 d4 = D4[4 * qb + i];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = 4 * i + j;
-          const int q = m0 + ro + j;
-          const float l2 = l4[j] * kLog2e;
-          float e, t = 0.f;
-          if constexpr (RAW) {
-            e = fast_exp2(__builtin_fmaf(S[qb][r], c2, -l2));
-          } else {
-            const float y = score_log2<SOFTCAP, ALIBI>(S[qb][r], p, slope_log2, q, my_kv, t);
-            e = fast_exp2(y - l2);
-          }
-          if (masked) {
-            // branch-free: every term evaluated, one select
-            const bool ok = (q < p.Sq) & (my_kv < p.Skv) & (!p.causal | (my_kv <= q)) &
-                            ((p.window == 0) | (q - my_kv <= p.window));
-            e = ok ? e : 0.f;
-          }
-          float ds = e * (DP[qb][r] - d4[j]);
-          if constexpr (SOFTCAP) ds *= 1.f - t * t;
-          pe[r] = e;
-          de[r] = ds;
-        }
-      }
-      pp[2 * qb] = pack8<T>(pe, 0);
-      pp[2 * qb + 1] = pack8<T>(pe, 8);
-      ps[2 * qb] = pack8<T>(de, 0);
-      ps[2 * qb + 1] = pack8<T>(de, 8);
+    for (int i = 0; i < 4; ++i) {
+      L4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 4 * h));
+      D4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 8 + 4 * h));
     }
   };
 
@@ -278,7 +241,7 @@ void bwd_kv_kernel(BwdArgs a) {
            (p.window > 0 && m0 + C::BM - 1 - kw0 > p.window);
   };
 
-  int cg = 0, cqt = qt_lo;  // tile being computed (head, query tile)
+  int cg = 0, cqt = qt_lo;  // tile whose P / dS is formed next (head, query tile)
   auto tile_info = [&](int& m0, float& slope) {
     const int hq = hk * p.G + cg;
     m0 = cqt * C::BM;
@@ -289,115 +252,197 @@ void bwd_kv_kernel(BwdArgs a) {
     }
   };
 
+  // P and log2-domain transform of element r (query row m0 + 8(r/4) + 4h +
+  // r%4, KV row my_kv); t = tanh for the soft-cap derivative.
+  auto p_elem = [&](const Set& x, int r, int m0, float sl, float& t) {
+    const float l2 = L4[r >> 2][r & 3] * kLog2e;
+    float sv = x.S[r];
+    pin(sv);  // read from the accumulator here, not hoisted into an earlier step
+    if constexpr (RAW) {
+      t = 0.f;
+      return fast_exp2(__builtin_fmaf(sv, c2, -l2));
+    } else {
+      const int q = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      const float y = score_log2<SOFTCAP, ALIBI>(sv, p, sl, q, my_kv, t);
+      return fast_exp2(y - l2);
+    }
+  };
+
+  // Masked recompute of P / dS of the tile in `cur` into `nxt` (rare).
+  auto valu_masked = [&](const Set& cur, int m0, float sl, Set& nxt) {
+    f32x16 pe, de;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int q = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      float t;
+      float e = p_elem(cur, r, m0, sl, t);
+      const bool ok = (q < p.Sq) & (my_kv < p.Skv) & (!p.causal | (my_kv <= q)) &
+                      ((p.window == 0) | (q - my_kv <= p.window));
+      e = ok ? e : 0.f;
+      float ds = e * (cur.DP[r] - D4[r >> 2][r & 3]);
+      if constexpr (SOFTCAP) ds *= 1.f - t * t;
+      pe[r] = e;
+      de[r] = ds;
+    }
+    nxt.PP[0] = pack8<T>(pe, 0);
+    nxt.PP[1] = pack8<T>(pe, 8);
+    nxt.PS[0] = pack8<T>(de, 0);
+    nxt.PS[1] = pack8<T>(de, 8);
+#pragma unroll
+    for (int i = 0; i < C::NPK; ++i) {  // kept inside the branch
+      pin(nxt.PP[i]);
+      pin(nxt.PS[i]);
+    }
+  };
+
+  // Row reads (A operands of S / dP) of the tile in stage st, MFMA k.
+  auto rdA = [&](int st, int k) {
+    const char* base = smem + st * C::STAGEB + (k & 1) * C::TILEB;
+    return lds_read16(base + koff[k >> 1]);
+  };
+  // Transpose reads (A operands of dV / dK) of the tile in stage st, MFMA j.
+  auto rdB = [&](int st, int j, i16x4& lo, i16x4& hi) {
+    const int db = (j >> 1) % C::DB, qc = (j >> 1) / C::DB;
+    const char* base = smem + st * C::STAGEB + ((j & 1) ? 0 : C::TILEB) + 16 * qc * C::ROWB;
+    lo = lds_read_tr4(base + voff_lo[db]);
+    hi = lds_read_tr4(base + voff_hi[db]);
+  };
+  auto mfma_kv = [&](int j, i16x4 lo, i16x4 hi, const Set& x) {
+    const int db = (j >> 1) % C::DB, qc = (j >> 1) / C::DB;
+    if (j & 1) dk[db] = M::mma(cat_tr<V8>(lo, hi), x.PS[qc], dk[db]);
+    else dv[db] = M::mma(cat_tr<V8>(lo, hi), x.PP[qc], dv[db]);
+  };
+
+  // S / dP of the tile in stage st into x (fills the pipeline).
+  auto fill = [&](int st, Set& x) {
+    i32x4 ab[5];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ab[k] = rdA(st, k);
+    x.S = f32x16{};
+    x.DP = f32x16{};
+#pragma unroll
+    for (int k = 0; k < 2 * C::KC; ++k) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (k + 4 < 2 * C::KC) ab[(k + 4) % 5] = rdA(st, k + 4);
+      if (k & 1) x.DP = M::mma(as_v8<V8>(ab[k % 5]), vreg[k >> 1], x.DP);
+      else x.S = M::mma(as_v8<V8>(ab[k % 5]), kreg[k >> 1], x.S);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // dV / dK of the tile in stage st with the packed P / dS of x (drains it).
+  auto drain = [&](int st, const Set& x) {
+    i16x4 blo[3], bhi[3];
+    rdB(st, 0, blo[0], bhi[0]);
+    rdB(st, 1, blo[1], bhi[1]);
+#pragma unroll
+    for (int j = 0; j < 4 * C::DB; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (j + 2 < 4 * C::DB) rdB(st, j + 2, blo[(j + 2) % 3], bhi[(j + 2) % 3]);
+      mfma_kv(j, blo[j % 3], bhi[j % 3], x);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  constexpr int CNT = 2 * C::E + 1;  // copy operations per tile per wave
+
+  // One pipeline iteration: the 16 S / dP MFMAs of tile u+1 (row reads four
+  // ahead), then the 16 dV / dK MFMAs of tile u-1 (transpose reads two
+  // ahead); every MFMA step carries half of one element of tile u's P / dS.
+  auto step = [&](int u, Set& cur, Set& nxt) {
+    wait_vmcnt<2 * CNT>();
+    __syncthreads();  // tile u+1 landed; stage (u - 4) % 8 no longer read
+    int m0;
+    float sl;
+    tile_info(m0, sl);
+    const int sn = (u + 1) & 7, sc = u & 7, sp = (u > 0 ? u - 1 : 0) & 7;
+    read_rows(sc);
+    i32x4 ab[5];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ab[k] = rdA(sn, k);
+    i16x4 blo[3], bhi[3];
+    nxt.S = f32x16{};
+    nxt.DP = f32x16{};
+    f32x16 pe, de;
+    float tt[16];
+    constexpr int NA = 2 * C::KC, NBK = 4 * C::DB;
+#pragma unroll
+    for (int k = 0; k < NA + NBK; ++k) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (k + 4 < NA) ab[(k + 4) % 5] = rdA(sn, k + 4);
+      if (k >= 1 && k <= 2 * C::E + 1) copy_op(u + 4, k - 1);  // copies of tile u+4
+      if (k >= NA - 2 && k - (NA - 2) < NBK) {
+        const int j = k - (NA - 2);
+        rdB(sp, j, blo[j % 3], bhi[j % 3]);
+      }
+      if (k < NA) {
+        if (k & 1) nxt.DP = M::mma(as_v8<V8>(ab[k % 5]), vreg[k >> 1], nxt.DP);
+        else nxt.S = M::mma(as_v8<V8>(ab[k % 5]), kreg[k >> 1], nxt.S);
+      } else {
+        const int j = k - NA;
+        mfma_kv(j, blo[j % 3], bhi[j % 3], cur);
+      }
+      const int r = k >> 1;
+      if (!(k & 1)) {
+        float t;
+        float e = p_elem(cur, r, m0, sl, t);
+        pin(e);  // formed in this step (not sunk below the MFMA run)
+        pe[r] = e;
+        tt[r] = t;
+      } else {
+        float dpv = cur.DP[r];
+        pin(dpv);
+        float ds = pe[r] * (dpv - D4[r >> 2][r & 3]);
+        if constexpr (SOFTCAP) ds *= 1.f - tt[r] * tt[r];
+        pin(ds);
+        de[r] = ds;
+        if (r == 7) {
+          nxt.PP[0] = pack8<T>(pe, 0);
+          nxt.PS[0] = pack8<T>(de, 0);
+          pin(nxt.PP[0]);
+          pin(nxt.PS[0]);
+        } else if (r == 15) {
+          nxt.PP[1] = pack8<T>(pe, 8);
+          nxt.PS[1] = pack8<T>(de, 8);
+          pin(nxt.PP[1]);
+          pin(nxt.PS[1]);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    advance();
+#pragma unroll
+    for (int i = 0; i < C::NPK; ++i) {  // fast path computed before the branch
+      pin(nxt.PP[i]);
+      pin(nxt.PS[i]);
+    }
+    if (need_mask(m0)) valu_masked(cur, m0, sl, nxt);
+  };
+
   if (ntile > 0) {
     issue(0);
     issue(1);
-    // u = 0: S / dP and P / dS only
-    {
-      wait_tile();
-      __syncthreads();
-      issue(2);
-      int m0;
-      float sl;
-      tile_info(m0, sl);
-      mma_s(0);
-      read_rows(0);
-      valu(m0, sl, false, PP, PS);
-      if (need_mask(m0)) valu(m0, sl, true, PP, PS);
+    issue(2);
+    issue(3);
+    wait_vmcnt<3 * CNT>();
+    __syncthreads();
+    fill(0, s0);
+#pragma unroll
+    for (int i = 0; i < C::NPK; ++i) {  // dV / dK of "tile -1" add zero
+      s0.PP[i] = V8{};
+      s0.PS[i] = V8{};
     }
-    for (int u = 1; u < ntile; ++u) {
-      wait_tile();
-      __syncthreads();  // tile u landed; stage (u - 2) % 4 no longer read
-      issue(u + 2);
-      int m0;
-      float sl;
-      tile_info(m0, sl);
-      const int st = u & 3, sp = (u - 1) & 3;
-      // Region A: S / dP MFMAs, row reads four steps ahead, then this tile's
-      // LSE / Delta rows.  Each step is fenced so the order is kept as written.
-      {
-        const char* sQ = smem + st * C::STAGEB;
-        const char* sO = sQ + C::TILEB;
-        constexpr int NA = 2 * C::KC;
-        auto rdA = [&](int k) { return lds_read16((k & 1 ? sO : sQ) + koff[k >> 1]); };
-        i32x4 ab[5];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) ab[k] = rdA(k);
-        S[0] = f32x16{};
-        DP[0] = f32x16{};
-#pragma unroll
-        for (int k = 0; k < NA; ++k) {
-          __builtin_amdgcn_sched_barrier(0);
-          if (k + 4 < NA) ab[(k + 4) % 5] = rdA(k + 4);
-          if (k & 1) DP[0] = M::mma(as_v8<V8>(ab[k % 5]), vreg[k >> 1], DP[0]);
-          else S[0] = M::mma(as_v8<V8>(ab[k % 5]), kreg[k >> 1], S[0]);
-          if (k == NA - 4) read_rows(st);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // Region B: dV / dK MFMAs of the previous tile, transpose reads two
-      // steps ahead; after MFMA k, element k of this tile's P and dS.
-      V8 PPn[C::NPK], PSn[C::NPK];
-      {
-        const char* sQp = smem + sp * C::STAGEB;
-        const char* sOp = sQp + C::TILEB;
-        constexpr int NB = 4 * C::QB * C::DB;
-        auto rdB = [&](int k, i16x4& lo, i16x4& hi) {
-          const int db = (k >> 1) % C::DB, qc = (k >> 1) / C::DB;
-          const char* base = ((k & 1) ? sQp : sOp) + 16 * qc * C::ROWB;
-          lo = lds_read_tr4(base + voff_lo[db]);
-          hi = lds_read_tr4(base + voff_hi[db]);
-        };
-        i16x4 blo[3], bhi[3];
-        rdB(0, blo[0], bhi[0]);
-        rdB(1, blo[1], bhi[1]);
-        f32x16 pe, de;
-#pragma unroll
-        for (int k = 0; k < NB; ++k) {
-          __builtin_amdgcn_sched_barrier(0);
-          if (k + 2 < NB) rdB(k + 2, blo[(k + 2) % 3], bhi[(k + 2) % 3]);
-          const int db = (k >> 1) % C::DB, qc = (k >> 1) / C::DB;
-          if (k & 1) dk[db] = M::mma(cat_tr<V8>(blo[k % 3], bhi[k % 3]), PS[qc], dk[db]);
-          else dv[db] = M::mma(cat_tr<V8>(blo[k % 3], bhi[k % 3]), PP[qc], dv[db]);
-          // element r = k of the current tile (one 32-row query block)
-          const int r = k, i = r >> 2, j = r & 3;
-          const int q = m0 + 8 * i + 4 * h + j;
-          const float l2 = L4[i][j] * kLog2e;
-          float e, t = 0.f;
-          if constexpr (RAW) {
-            e = fast_exp2(__builtin_fmaf(S[0][r], c2, -l2));
-          } else {
-            const float y = score_log2<SOFTCAP, ALIBI>(S[0][r], p, sl, q, my_kv, t);
-            e = fast_exp2(y - l2);
-          }
-          float ds = e * (DP[0][r] - D4[i][j]);
-          if constexpr (SOFTCAP) ds *= 1.f - t * t;
-          pe[r] = e;
-          de[r] = ds;
-          if (r == 7) {
-            PPn[0] = pack8<T>(pe, 0);
-            PSn[0] = pack8<T>(de, 0);
-          } else if (r == 15) {
-            PPn[1] = pack8<T>(pe, 8);
-            PSn[1] = pack8<T>(de, 8);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // fast-path P / dS stay computed here (not sunk into the branch below)
-#pragma unroll
-      for (int i = 0; i < C::NPK; ++i) {
-        pin(PPn[i]);
-        pin(PSn[i]);
-      }
-      if (need_mask(m0)) valu(m0, sl, true, PPn, PSn);
-#pragma unroll
-      for (int i = 0; i < C::NPK; ++i) {
-        PP[i] = PPn[i];
-        PS[i] = PSn[i];
-      }
+    int u = 0;
+    for (; u + 2 <= ntile; u += 2) {
+      step(u, s0, s1);
+      step(u + 1, s1, s0);
     }
-    mma_kv((ntile - 1) & 3);
+    if (u < ntile) {
+      step(u, s0, s1);
+      drain((ntile - 1) & 7, s1);
+    } else {
+      drain((ntile - 1) & 7, s0);
+    }
     wait_vmcnt<0>();  // redundant copies in flight must land before the workgroup ends
   }
 
