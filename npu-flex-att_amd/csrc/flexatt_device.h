@@ -106,6 +106,12 @@ template <class X>
 __device__ __forceinline__ void pin(X& x) {
   asm volatile("" : "+v"(x));
 }
+// Read-only form: x must be in a VGPR at this point (e.g. read out of an
+// accumulator register here), without a copy for the later uses.
+template <class X>
+__device__ __forceinline__ void pin_in(const X& x) {
+  asm volatile("" ::"v"(x));
+}
 
 // --- direct global -> LDS tile staging --------------------------------------
 // global_load_lds_dwordx4: lane l's 16 bytes land at LDS byte address
@@ -153,20 +159,22 @@ __device__ __forceinline__ int swz_tr_inv(int r, int p) {
   else return (p - 4 * r) & (CPR - 1);
 }
 
-// One layout for tiles that are read both ways: 16-byte column reads (rows
-// as MFMA A operands) and transpose reads (columns as A operands).  Chunk c
-// of row r sits at chunk (c + 2r + bit3(r)) mod CPR: conflict-free for both
-// patterns (measured 255 B/clk/CU for the b128 reads and 126 B/clk/CU for the
-// transpose reads, each the LDS peak for that width).
+// One layout for tiles that are read both ways: 16-byte row reads (rows as
+// MFMA operands; 16 lanes per LDS cycle read one chunk of 16 consecutive
+// rows) and transpose reads (32 lanes per LDS cycle read chunks 4j..4j+3 of
+// 4 consecutive rows 4i..4i+3).  Chunk c of row r sits at chunk c ^ g(r),
+// g(r) = (r mod 4) * 4 + (r / 4) mod 4: g is a permutation over any 16
+// consecutive rows (row reads hit 16 distinct bank groups) and 4 consecutive
+// rows differ in the top two bits of g (a transpose read's 16 chunks land in
+// 16 distinct bank groups).  The swizzle is its own inverse.
 template <int CPR>
 __device__ __forceinline__ int swz_dual(int r, int c) {
   static_assert(CPR == 16, "dual-use swizzle is defined for 256-byte rows");
-  return (c + 2 * r + ((r >> 3) & 1)) & (CPR - 1);
+  return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
 }
 template <int CPR>
 __device__ __forceinline__ int swz_dual_inv(int r, int p) {
-  static_assert(CPR == 16, "dual-use swizzle is defined for 256-byte rows");
-  return (p - 2 * r - ((r >> 3) & 1)) & (CPR - 1);
+  return swz_dual<CPR>(r, p);
 }
 
 // Value of lane l ^ 32 (the other half of the wave).
