@@ -109,6 +109,11 @@ void bwd_kv_kernel(BwdArgs a) {
   const int qt_lo = q_lo / C::BM;
   const int nqt = q_hi > q_lo ? (q_hi + C::BM - 1) / C::BM - qt_lo : 0;
   const int ntile = p.G * nqt;
+  // Tile order: query tiles from the last one down, the G heads of a query
+  // tile consecutively.  All KV blocks of one (b, hkv) run together on one
+  // XCD and start at the same (last) query tile, so they walk the Q / dO
+  // stream in step and each tile is fetched from HBM about once.
+  const int qt_top = qt_lo + nqt - 1;
 
   // Lane-constant LDS byte offsets of the row reads (S-wave) and the
   // transpose reads (KV-wave) within a tile.
@@ -147,7 +152,7 @@ void bwd_kv_kernel(BwdArgs a) {
     constexpr bool RAW = !SOFTCAP && !ALIBI;
     const float c2 = p.scale_log2;
     const bool kv_tail = kw0 + 32 > p.Skv;
-    int cg = 0, cqt = qt_lo;  // tile being formed (head, query tile)
+    int cg = 0, cqt = qt_top;  // tile being formed (head, query tile)
     int sc = 0;               // its stage
 
     __syncthreads();  // prologue: tile 0 landed, its LSE in log2 units
@@ -186,9 +191,9 @@ void bwd_kv_kernel(BwdArgs a) {
         const int hq = hk * p.G + cg;
         const int m0 = cqt * C::BM;
         const float sl = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
-        if (++cqt == qt_lo + nqt) {
-          cqt = qt_lo;
-          ++cg;
+        if (++cg == p.G) {
+          cg = 0;
+          --cqt;
         }
         // LSE (log2 units) and Delta of this lane's query rows m0 + 8i + 4h + j.
         const float* sR = (const float*)(smem + sc * C::STAGEB + 2 * C::TILEB);
@@ -270,26 +275,29 @@ void bwd_kv_kernel(BwdArgs a) {
       }
       crl = min(rl, last);
     };
-    const int64_t qstep = (int64_t)C::BM * a.q.ss * (int64_t)sizeof(T);
-    const int64_t ostep = (int64_t)C::BM * a.dout.ss * (int64_t)sizeof(T);
-    int is_g = 0, is_qt = qt_lo;  // next tile to copy (head, query tile)
+    // Byte steps: to the next head of the group, and from the last head of a
+    // query tile back to the first head of the query tile below.
+    const int64_t qh = a.q.sh * (int64_t)sizeof(T), oh = a.dout.sh * (int64_t)sizeof(T);
+    const int64_t qback = (int64_t)(p.G - 1) * qh + (int64_t)C::BM * a.q.ss * (int64_t)sizeof(T);
+    const int64_t oback = (int64_t)(p.G - 1) * oh + (int64_t)C::BM * a.dout.ss * (int64_t)sizeof(T);
+    const int64_t lback = (int64_t)(p.G - 1) * p.Sq + C::BM;
+    int is_g = 0, is_qt = qt_top;  // next tile to copy (head, query tile)
     const char *qcur, *ocur;
     const float* lcur;  // LSE (lanes 0-7) or Delta (lanes 8-15) row m0
-    bool tail = false;
-    auto set_head = [&](int g) {
-      const int hq = hk * p.G + g;
-      const int64_t m0 = (int64_t)qt_lo * C::BM;
+    {
+      const int hq = hk * p.G;
+      const int64_t m0 = (int64_t)qt_top * C::BM;
       qcur = (const char*)((const T*)a.q.data + b * a.q.sb + hq * a.q.sh + m0 * a.q.ss);
       ocur = (const char*)((const T*)a.dout.data + b * a.dout.sb + hq * a.dout.sh + m0 * a.dout.ss);
       lcur = (lane < 8 ? a.lse : a.delta) + (int64_t)(b * p.Hq + hq) * p.Sq + m0;
-    };
-    auto prep = [&]() {
+    }
+    bool tail = false;
+    auto prep = [&]() {  // per-lane offsets for the query tile is_qt
       const int m0 = is_qt * C::BM;
       const bool t = m0 + C::BM > p.Sq;
       if (t || tail) set_offsets(t ? p.Sq - 1 - m0 : C::BM);
       tail = t;
     };
-    set_head(0);
     set_offsets(C::BM);
     prep();
     // Copy operation j (0 .. 2E) of the next tile, going to stage st.
@@ -304,16 +312,19 @@ void bwd_kv_kernel(BwdArgs a) {
       }
     };
     auto advance = [&]() {  // past the end the last tile is copied again
-      if (is_g < p.G - 1 || is_qt < qt_lo + nqt - 1) {
-        if (++is_qt == qt_lo + nqt) {
-          is_qt = qt_lo;
-          set_head(++is_g);
+      if (is_g < p.G - 1 || is_qt > qt_lo) {
+        if (++is_g == p.G) {
+          is_g = 0;
+          --is_qt;
+          qcur -= qback;
+          ocur -= oback;
+          lcur -= lback;
+          prep();
         } else {
-          qcur += qstep;
-          ocur += ostep;
-          lcur += C::BM;
+          qcur += qh;
+          ocur += oh;
+          lcur += p.Sq;
         }
-        prep();
       }
     };
     constexpr int CNT = 2 * C::E + 1;  // copy operations per tile per KV-wave

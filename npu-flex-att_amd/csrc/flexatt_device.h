@@ -30,6 +30,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -254,6 +255,14 @@ __device__ __forceinline__ void sum8(typename Mfma<T>::v8 p, float (&acc)[4]) {
   acc[1] = Dot2<T>::add(__builtin_shufflevector(p, p, 2, 3), acc[1]);
   acc[2] = Dot2<T>::add(__builtin_shufflevector(p, p, 4, 5), acc[2]);
   acc[3] = Dot2<T>::add(__builtin_shufflevector(p, p, 6, 7), acc[3]);
+}
+
+// Two fp32 values rounded to T, packed into one 32-bit word (a in the low half).
+template <class T>
+__device__ __forceinline__ unsigned pk2(float a, float b) {
+  typedef T x2 __attribute__((ext_vector_type(2)));
+  const x2 v = {from_f32<T>(a), from_f32<T>(b)};
+  return __builtin_bit_cast(unsigned, v);
 }
 
 // Pack 4 fp32 values into 4 x T (8 bytes) for a store.
