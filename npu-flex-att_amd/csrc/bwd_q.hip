@@ -131,15 +131,46 @@ void bwd_q_kernel(BwdArgs a) {
     crow[e] = q / C::CPR;
     cchk[e] = swz_dual_inv<C::CPR>(crow[e], q % C::CPR);
   }
-  auto issue = [&](int u) {
-    const unsigned sb = lds0 + (u & 3) * C::STAGEB;
-    const int n0 = min(t_lo + u, t_hi - 1) * C::BN;
+  // Per tile only the scalar bases move; the per-lane byte offsets are
+  // recomputed (clamped to row Skv - 1) only for a KV-tail tile.
+  int64_t ko[C::E], vo[C::E];
+  auto set_offsets = [&](int last) {  // last = Skv - 1 - n0 (clamp)
 #pragma unroll
     for (int e = 0; e < C::E; ++e) {
-      const int64_t r = min(n0 + crow[e], p.Skv - 1);
+      const int64_t r = min(crow[e], last);
+      ko[e] = (r * a.k.ss + cchk[e] * 8) * (int64_t)sizeof(T);
+      vo[e] = (r * a.v.ss + cchk[e] * 8) * (int64_t)sizeof(T);
+    }
+  };
+  const int64_t kstep = (int64_t)C::BN * a.k.ss * (int64_t)sizeof(T);
+  const int64_t vstep = (int64_t)C::BN * a.v.ss * (int64_t)sizeof(T);
+  int ct = t_lo;  // tile the next issue() copies
+  const char* kcur = (const char*)(kp + (int64_t)t_lo * C::BN * a.k.ss);
+  const char* vcur = (const char*)(vp + (int64_t)t_lo * C::BN * a.v.ss);
+  bool ctail = false;
+  auto prep = [&]() {
+    const int n0 = ct * C::BN;
+    const bool t = n0 + C::BN > p.Skv;
+    if (t || ctail) set_offsets(t ? p.Skv - 1 - n0 : C::BN);
+    ctail = t;
+  };
+  set_offsets(C::BN);
+  prep();
+  // issue(u) copies tile t_lo + u into stage u % 4 (calls come in order of u;
+  // past the end the last tile is copied again).
+  auto issue = [&](int u) {
+    const unsigned sb = lds0 + (u & 3) * C::STAGEB;
+#pragma unroll
+    for (int e = 0; e < C::E; ++e) {
       const unsigned dst = sb + (wave * C::E + e) * 1024;
-      load_lds16(kp + r * a.k.ss + cchk[e] * 8, dst);
-      load_lds16(vp + r * a.v.ss + cchk[e] * 8, dst + C::TILEB);
+      load_lds16(kcur + ko[e], dst);
+      load_lds16(vcur + vo[e], dst + C::TILEB);
+    }
+    if (ct < t_hi - 1) {
+      ++ct;
+      kcur += kstep;
+      vcur += vstep;
+      prep();
     }
   };
   auto wait_tile = [&]() { wait_vmcnt<2 * C::E>(); };
