@@ -1,5 +1,5 @@
 // Flash-attention backward dQ for fp16/bf16 on gfx950 MFMA (query-stationary
-// tile stream).
+// tile stream, KV-split wave pairs).
 //
 // Semantics: npu_flash_attention.py:298-402 (flash_attn_bwd_dq_kernel): P is
 // recomputed from the forward LSE (including the ALiBi bias, which the
@@ -8,27 +8,26 @@
 // input dtype before its MFMA, as the reference does before tl.dot.
 //
 // Decomposition
-//  * One workgroup = 4 waves (one per SIMD, the whole register file each) =
-//    one (batch, KV head), gp query heads that share it (gp = the largest power
-//    of two dividing G, at most 4) and 32 * 4 / gp query rows of each.  Each
-//    wave owns 32 query rows of one head and each lane one query row: its Q
-//    and dO rows stay in registers as MFMA B operands and its LSE and Delta
-//    are one scalar each.
-//  * S^T = K Q^T and dP^T = V dO^T per 32-row block of a 64-row KV tile (A =
-//    K / V rows from LDS); dQ^T += K^T dS^T with K^T read by the LDS transpose
-//    read, so the K tile is read both ways (dual-use swizzle).
-//  * K / V tiles are copied global -> LDS with direct-to-LDS loads two tiles
-//    ahead into four stages, one barrier per tile.
-//  * Software pipeline inside each wave, each step in a fixed order: the S^T
-//    MFMAs of tile t, then its dP^T MFMAs with P = exp2(y - LSE) formed in
-//    their shadow, then the dQ MFMAs of tile t-1 with dS of tile t formed in
-//    theirs.
-//  * Tiles that cross the causal diagonal, the window edge or the KV tail for
-//    some row of a wave take the fast path first and then recompute dS with
-//    the per-element mask (only the packed dS registers differ between the
-//    paths, so the accumulators never sit on two code paths).
-// Deterministic: every output element is owned by one lane and accumulated in
-// a fixed order.
+//  * One workgroup = 8 waves for one (batch, KV head): gp query heads that
+//    share it (gp = the largest power of two dividing G, at most 4) and
+//    32 * 4 / gp query rows of each.  Query slot s (32 rows of one head) is
+//    owned by the wave pair s, s + 4, which share a SIMD: lane = query row, the
+//    Q and dO rows in registers as MFMA B operands in both waves.  Each 64-row
+//    KV tile is split between the pair: wave s takes KV rows 0-31, wave s + 4
+//    rows 32-63.  Each wave accumulates its own partial dQ^T; the two partials
+//    are added once, through LDS, at the end (fixed order: deterministic).
+//  * Per tile and wave: S^T = K Q^T and dP^T = V dO^T for its 32 KV rows (A =
+//    K / V rows from LDS, 16 MFMAs), P and dS on the VALU, then
+//    dQ^T += K^T dS^T (8 MFMAs, K^T read with the LDS transpose read from the
+//    same swizzled K tile).
+//  * Ping-pong: the two halves run the same program one phase apart.  An MFMA
+//    phase issues the S / dP MFMAs of tile t and the dQ MFMAs of tile t-1
+//    (24 independent MFMAs); a VALU phase forms P and dS of tile t.  While
+//    one wave of a SIMD streams MFMAs the other runs its VALU phase.
+//  * K / V tiles are copied global -> LDS with direct-to-LDS loads three tiles
+//    ahead into four stages; every phase ends with a workgroup barrier.
+// Deterministic: every output element is owned by one lane pair and
+// accumulated in a fixed order.
 #include "flexatt_device.h"
 #include "flexatt_kernels.h"
 
@@ -42,9 +41,9 @@ namespace flexatt {
 
 template <int D>
 struct QCfg {
-  static constexpr int NW = 4;       // waves per workgroup, one per SIMD
-  static constexpr int BN = 64;      // KV rows per tile
-  static constexpr int NB = BN / 32;
+  static constexpr int NS = 4;        // query slots per workgroup (one per SIMD)
+  static constexpr int NW = 2 * NS;   // waves: slot s and s + 4 split each KV tile
+  static constexpr int BN = 64;       // KV rows per tile (32 per wave)
   static constexpr int KC = D / 16;
   static constexpr int DB = D / 32;
   static constexpr int CPR = D / 8;
@@ -53,28 +52,30 @@ struct QCfg {
   static constexpr int E = TILEB / (1024 * NW);   // 1 KB copies per wave per tensor
   static constexpr int STAGEB = 2 * TILEB;
   static constexpr int STAGES = 4;
-  static constexpr int NPK = 2 * NB;              // packed dS operands per tile
   static_assert(E * 1024 * NW == TILEB, "tile must split into 1 KB copies");
+  static_assert(NS * 64 * 64 * 4 <= STAGES * STAGEB, "the partial-dQ exchange fits in the stage memory");
 };
 
 template <class T, int D, bool SOFTCAP, bool ALIBI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void bwd_q_kernel(BwdArgs a) {
   using C = QCfg<D>;
   using M = Mfma<T>;
   using V8 = typename M::v8;
-  static_assert(C::NB == 2 && C::KC == 8 && C::DB == 4, "the hand-ordered step assumes D = 128, 64-row tiles");
+  static_assert(C::KC == 8 && C::DB == 4, "the phase layout assumes D = 128");
   __shared__ __attribute__((aligned(1024))) char smem[C::STAGES * C::STAGEB];
 
   const Shape& p = a.p;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int slot = wave & (C::NS - 1);
+  const int grp = wave >> 2;  // KV half of each tile; also the ping-pong group
   const int h = lane >> 5, l32 = lane & 31;
 
   // Work item: (b, hkv, head group, q-tile); the longest causal tiles first.
   const int gp = a.ntiles & 0xff;   // heads per workgroup (set by the launcher)
   const int nqt = a.ntiles >> 8;    // query tiles per head
-  const int bmh = 32 * (C::NW / gp);
+  const int bmh = 32 * (C::NS / gp);
   const int w = xcd_remap(blockIdx.x, gridDim.x);
   const int qt = nqt - 1 - (w % nqt);
   int rest = w / nqt;
@@ -82,9 +83,9 @@ void bwd_q_kernel(BwdArgs a) {
   const int gs = rest % ngs;
   rest /= ngs;
   const int hk = rest % p.Hkv, b = rest / p.Hkv;
-  const int hq = hk * p.G + gs * gp + wave % gp;
+  const int hq = hk * p.G + gs * gp + slot % gp;
   const int m0 = qt * bmh;
-  const int mw = m0 + 32 * (wave / gp);  // first query row of this wave
+  const int mw = m0 + 32 * (slot / gp);  // first query row of this slot
   const int my_m = mw + l32;             // query row of this lane
 
   // Q / dO rows as MFMA B operands; LSE (log2) and Delta of this lane's row.
@@ -144,7 +145,7 @@ void bwd_q_kernel(BwdArgs a) {
   };
   const int64_t kstep = (int64_t)C::BN * a.k.ss * (int64_t)sizeof(T);
   const int64_t vstep = (int64_t)C::BN * a.v.ss * (int64_t)sizeof(T);
-  int ct = t_lo;  // tile the next issue() copies
+  int ct = t_lo, cst = 0;  // tile the next copy takes, and its stage
   const char* kcur = (const char*)(kp + (int64_t)t_lo * C::BN * a.k.ss);
   const char* vcur = (const char*)(vp + (int64_t)t_lo * C::BN * a.v.ss);
   bool ctail = false;
@@ -156,16 +157,17 @@ void bwd_q_kernel(BwdArgs a) {
   };
   set_offsets(C::BN);
   prep();
-  // issue(u) copies tile t_lo + u into stage u % 4 (calls come in order of u;
-  // past the end the last tile is copied again).
-  auto issue = [&](int u) {
-    const unsigned sb = lds0 + (u & 3) * C::STAGEB;
+  // Copies of the next tile in order (past the end the last tile is copied
+  // again into the next stage).
+  auto issue_next = [&]() {
+    const unsigned sb = lds0 + cst * C::STAGEB;
 #pragma unroll
     for (int e = 0; e < C::E; ++e) {
       const unsigned dst = sb + (wave * C::E + e) * 1024;
       load_lds16(kcur + ko[e], dst);
       load_lds16(vcur + vo[e], dst + C::TILEB);
     }
+    cst = (cst + 1) & 3;
     if (ct < t_hi - 1) {
       ++ct;
       kcur += kstep;
@@ -175,19 +177,22 @@ void bwd_q_kernel(BwdArgs a) {
   };
   auto wait_tile = [&]() { wait_vmcnt<2 * C::E>(); };
 
-  // Lane-constant LDS byte offsets (row reads, and transpose reads of rows
-  // r and r + 8 of each 16-row group).
+  // Lane-constant LDS byte offsets of this wave's KV half: row reads (A
+  // operands of S^T / dP^T) and transpose reads of rows r and r + 8 of each
+  // 16-row group (A operands of dQ^T).
+  const int hrow = 32 * grp;
   int koff[C::KC], voff_lo[C::DB], voff_hi[C::DB];
 #pragma unroll
-  for (int kc = 0; kc < C::KC; ++kc) koff[kc] = l32 * C::ROWB + swz_dual<C::CPR>(l32, 2 * kc + h) * 16;
+  for (int kc = 0; kc < C::KC; ++kc)
+    koff[kc] = (hrow + l32) * C::ROWB + swz_dual<C::CPR>(hrow + l32, 2 * kc + h) * 16;
   {
     const int tr_row = 4 * h + ((lane & 15) >> 2);
     const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
     for (int db = 0; db < C::DB; ++db) {
       const int c = 4 * db + (tr_col >> 3), e2 = (tr_col & 7) * 2;
-      voff_lo[db] = tr_row * C::ROWB + swz_dual<C::CPR>(tr_row, c) * 16 + e2;
-      voff_hi[db] = (tr_row + 8) * C::ROWB + swz_dual<C::CPR>(tr_row + 8, c) * 16 + e2;
+      voff_lo[db] = (hrow + tr_row) * C::ROWB + swz_dual<C::CPR>(hrow + tr_row, c) * 16 + e2;
+      voff_hi[db] = (hrow + tr_row + 8) * C::ROWB + swz_dual<C::CPR>(hrow + tr_row + 8, c) * 16 + e2;
     }
   }
 
@@ -195,183 +200,154 @@ void bwd_q_kernel(BwdArgs a) {
   const float c2 = p.scale_log2;
   const float slope_log2 = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
 
-  // Tiles [tm_lo, tm_hi) are fully allowed for every row of this wave.
-  int tm_hi = p.Skv / C::BN;
-  if (p.causal) tm_hi = min(tm_hi, (mw + 1) / C::BN);
-  int tm_lo = 0;
-  if (p.window > 0) tm_lo = max(0, (mw + 31 - p.window + C::BN - 1) / C::BN);
-  tm_hi = __builtin_amdgcn_readfirstlane(tm_hi);
-  tm_lo = __builtin_amdgcn_readfirstlane(tm_lo);
+  f32x16 S, DP;  // S^T and dP^T of this wave's 32 KV rows of the current tile
+  V8 PS[2];      // packed dS^T of the previous tile (KV rows 0-15, 16-31 of the half)
 
-  f32x16 S[C::NB], DP[C::NB];  // S^T and dP^T of the tile being processed
-  f32x16 PE[C::NB];            // P^T of that tile
-  V8 PS[C::NPK];               // packed dS^T of the previous tile
-
-  // Element r of block bb of the current tile (KV row n0 + 32bb + 8(r/4) +
-  // 4h + r%4, query row my_m): P, and t = tanh for the soft-cap derivative.
-  auto p_elem = [&](int bb, int r, int n0, float& t) {
-    if constexpr (RAW) {
-      t = 0.f;
-      return fast_exp2(__builtin_fmaf(S[bb][r], c2, -lse2));
-    } else {
-      const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
-      const float y = score_log2<SOFTCAP, ALIBI>(S[bb][r], p, slope_log2, my_m, j, t);
-      return fast_exp2(y - lse2);
-    }
-  };
-  float TT[C::NB][16];  // tanh values (soft-cap only; unused otherwise)
-  auto ds_elem = [&](int bb, int r) {
-    float ds = PE[bb][r] * (DP[bb][r] - dlt);
-    if constexpr (SOFTCAP) ds *= 1.f - TT[bb][r] * TT[bb][r];
-    return ds;
-  };
-  // Masked recompute of dS for a tile that needs the per-element mask.
-  auto ds_masked = [&](int n0, V8 (&ps)[C::NPK]) {
-#pragma unroll
-    for (int bb = 0; bb < C::NB; ++bb) {
+  // VALU phase: P and dS of the tile at KV row n0 (element r is KV row
+  // n0 + hrow + 8(r/4) + 4h + r%4, query row my_m).
+  auto vphase = [&](int n0) {
+    const int kw = n0 + hrow;  // first KV row of this wave's half
+    const bool full = (kw + 32 <= p.Skv) && (!p.causal || kw + 31 <= mw) &&
+                      (p.window == 0 || mw + 31 - kw <= p.window);
+    int jb = kw + 4 * h;  // pinned: no per-element index is hoisted and kept live
+    pin(jb);
+    auto form = [&](auto masked) {
       f32x16 de;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
-        const bool ok = (j < p.Skv) & (!p.causal | (j <= my_m)) & ((p.window == 0) | (my_m - j <= p.window));
-        const float ds = ds_elem(bb, r);
-        de[r] = ok ? ds : 0.f;
+        float t = 0.f, e;
+        const int j = jb + 8 * (r >> 2) + (r & 3);
+        if constexpr (RAW) {
+          e = fast_exp2(__builtin_fmaf(S[r], c2, -lse2));
+        } else {
+          const float y = score_log2<SOFTCAP, ALIBI>(S[r], p, slope_log2, my_m, j, t);
+          e = fast_exp2(y - lse2);
+        }
+        if constexpr (decltype(masked)::value) {
+          const bool ok = (j < p.Skv) & (!p.causal | (j <= my_m)) & ((p.window == 0) | (my_m - j <= p.window));
+          e = ok ? e : 0.f;
+        }
+        float ds = e * (DP[r] - dlt);
+        if constexpr (SOFTCAP) ds *= 1.f - t * t;
+        de[r] = ds;
       }
-      ps[2 * bb] = pack8<T>(de, 0);
-      ps[2 * bb + 1] = pack8<T>(de, 8);
-    }
-    // results fixed inside the (rarely taken) branch, so that the compiler
-    // keeps it a branch instead of computing it on every tile and selecting
-#pragma unroll
-    for (int i = 0; i < C::NPK; ++i) pin(ps[i]);
+      PS[0] = pack8<T>(de, 0);
+      PS[1] = pack8<T>(de, 8);
+    };
+    if (full)
+      form(std::false_type{});
+    else
+      form(std::true_type{});
+    // done before the barrier
+    pin(PS[0]);
+    pin(PS[1]);
   };
 
-  // Region A1 + A2 for the tile in stage st: S^T MFMAs (row reads of K four
-  // ahead), then dP^T MFMAs (row reads of V four ahead) with P formed in
-  // their shadow.
-  auto regions_a = [&](int st, int n0) {
-    const char* sK = smem + st * C::STAGEB;
-    const char* sV = sK + C::TILEB;
-    constexpr int NA = C::NB * C::KC;  // 16
-    auto rdK = [&](int k) { return lds_read16(sK + (k & 1) * 32 * C::ROWB + koff[k >> 1]); };
-    auto rdV = [&](int k) { return lds_read16(sV + (k & 1) * 32 * C::ROWB + koff[k >> 1]); };
-    i32x4 ab[5];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) ab[k] = rdK(k);
-#pragma unroll
-    for (int bb = 0; bb < C::NB; ++bb) {
-      S[bb] = f32x16{};
-      DP[bb] = f32x16{};
-    }
-#pragma unroll
-    for (int k = 0; k < NA; ++k) {
-      __builtin_amdgcn_sched_barrier(0);
-      if (k + 4 < NA) ab[(k + 4) % 5] = rdK(k + 4);
-      else ab[(k + 4) % 5] = rdV(k + 4 - NA);
-      S[k & 1] = M::mma(as_v8<V8>(ab[k % 5]), qf[k >> 1], S[k & 1]);
-    }
-    // the read ring continues: V read k sits at ring position (NA + k) % 5
-#pragma unroll
-    for (int k = 0; k < NA; ++k) {
-      __builtin_amdgcn_sched_barrier(0);
-      if (k + 4 < NA) ab[(NA + k + 4) % 5] = rdV(k + 4);
-      DP[k & 1] = M::mma(as_v8<V8>(ab[(NA + k) % 5]), df[k >> 1], DP[k & 1]);
-      // two elements of P per MFMA (both S^T blocks are complete by now)
-#pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        const int idx = 2 * k + x, bb = idx >> 4, r = idx & 15;
-        float t;
-        PE[bb][r] = p_elem(bb, r, n0, t);
-        if constexpr (SOFTCAP) TT[bb][r] = t;
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // Region B: dQ^T MFMAs of the tile in stage sp with PS (transpose reads of K
-  // two ahead); after MFMA k, two elements of the current tile's dS.
-  auto region_b = [&](int sp, bool do_ds, V8 (&psn)[C::NPK]) {
-    const char* sKp = smem + sp * C::STAGEB;
-    constexpr int NBQ = C::DB * C::NPK;  // 16
-    auto rdB = [&](int k, i16x4& lo, i16x4& hi) {
-      const int db = k % C::DB, c16 = k / C::DB;  // 16-row KV chunk
-      const char* base = sKp + 16 * c16 * C::ROWB;
+  // MFMA phase: S^T / dP^T of the tile in stage sk (DO_S) and dQ^T of the
+  // previous tile in stage sq with PS (DO_Q): a dQ MFMA after every second
+  // S / dP MFMA.  Row reads are kept four MFMAs ahead, transpose reads two
+  // dQ MFMAs ahead.
+  auto mphase = [&](auto do_s_c, auto do_q_c, int sk, int sq) {
+    constexpr bool DO_S = decltype(do_s_c)::value, DO_Q = decltype(do_q_c)::value;
+    const char* sK = smem + sk * C::STAGEB;
+    const char* sQ = smem + sq * C::STAGEB;
+    auto rdA = [&](int k) {  // k even: K row chunk k/2, odd: V row chunk k/2
+      return lds_read16(sK + (k & 1) * C::TILEB + koff[k >> 1]);
+    };
+    auto rdB = [&](int j, i16x4& lo, i16x4& hi) {
+      const int db = j % C::DB, c16 = j / C::DB;
+      const char* base = sQ + 16 * c16 * C::ROWB;
       lo = lds_read_tr4(base + voff_lo[db]);
       hi = lds_read_tr4(base + voff_hi[db]);
     };
+    i32x4 ab[5];
     i16x4 blo[3], bhi[3];
-    rdB(0, blo[0], bhi[0]);
-    rdB(1, blo[1], bhi[1]);
-    f32x16 de[C::NB];
+    if constexpr (DO_S) {
 #pragma unroll
-    for (int k = 0; k < NBQ; ++k) {
+      for (int k = 0; k < 4; ++k) ab[k] = rdA(k);
+      S = f32x16{};
+      DP = f32x16{};
+    }
+    if constexpr (DO_Q) {
+      rdB(0, blo[0], bhi[0]);
+      rdB(1, blo[1], bhi[1]);
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
       __builtin_amdgcn_sched_barrier(0);
-      if (k + 2 < NBQ) rdB(k + 2, blo[(k + 2) % 3], bhi[(k + 2) % 3]);
-      const int db = k % C::DB, c16 = k / C::DB;
-      dq[db] = M::mma(cat_tr<V8>(blo[k % 3], bhi[k % 3]), PS[c16], dq[db]);
-      if (do_ds) {
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          const int idx = 2 * k + x, bb = idx >> 4, r = idx & 15;
-          de[bb][r] = ds_elem(bb, r);
-          if (r == 15) {
-            psn[2 * bb] = pack8<T>(de[bb], 0);
-            psn[2 * bb + 1] = pack8<T>(de[bb], 8);
-          }
+      if constexpr (DO_S) {
+        if (k + 4 < 16) ab[(k + 4) % 5] = rdA(k + 4);
+        if (k & 1) DP = M::mma(as_v8<V8>(ab[k % 5]), df[k >> 1], DP);
+        else S = M::mma(as_v8<V8>(ab[k % 5]), qf[k >> 1], S);
+      }
+      if constexpr (DO_Q) {
+        if (k & 1) {
+          const int j = k >> 1;
+          if (j + 2 < 8) rdB(j + 2, blo[(j + 2) % 3], bhi[(j + 2) % 3]);
+          const int db = j % C::DB, c16 = j / C::DB;
+          dq[db] = M::mma(cat_tr<V8>(blo[j % 3], bhi[j % 3]), PS[c16], dq[db]);
         }
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (DO_S) {  // results fixed before the barrier
+      pin(S);
+      pin(DP);
+    }
   };
 
   if (nt > 0) {
-    issue(0);
-    issue(1);
-    {
+    issue_next();  // t_lo
+    issue_next();  // t_lo + 1
+    wait_tile();
+    __syncthreads();
+    if (grp) __syncthreads();  // second half starts one phase late
+    issue_next();  // t_lo + 2
+    mphase(std::true_type{}, std::false_type{}, 0, 0);
+    wait_tile();
+    __syncthreads();
+    for (int u = 0; u + 1 < nt; ++u) {
+      vphase((t_lo + u) * C::BN);
       wait_tile();
       __syncthreads();
-      issue(2);
-      const int n0 = t_lo * C::BN;
-      regions_a(0, n0);
-#pragma unroll
-      for (int bb = 0; bb < C::NB; ++bb) {
-        f32x16 de;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) de[r] = ds_elem(bb, r);
-        PS[2 * bb] = pack8<T>(de, 0);
-        PS[2 * bb + 1] = pack8<T>(de, 8);
-      }
-      if (t_lo < tm_lo || t_lo >= tm_hi) ds_masked(n0, PS);
-    }
-    for (int u = 1; u < nt; ++u) {
+      issue_next();  // t_lo + u + 3
+      mphase(std::true_type{}, std::true_type{}, (u + 1) & 3, u & 3);
       wait_tile();
-      __syncthreads();  // tile u landed; stage (u - 2) % 4 no longer read
-      issue(u + 2);
-      const int t = t_lo + u, n0 = t * C::BN;
-      regions_a(u & 3, n0);
-      V8 PSn[C::NPK];
-      region_b((u - 1) & 3, true, PSn);
-#pragma unroll
-      for (int i = 0; i < C::NPK; ++i) pin(PSn[i]);  // fast path computed before the branch
-      if (t < tm_lo || t >= tm_hi) ds_masked(n0, PSn);
-#pragma unroll
-      for (int i = 0; i < C::NPK; ++i) PS[i] = PSn[i];
+      __syncthreads();
     }
-    V8 unused[C::NPK];
-    region_b((nt - 1) & 3, false, unused);
-    wait_vmcnt<0>();  // redundant copies in flight must land before the workgroup ends
+    vphase((t_hi - 1) * C::BN);
+    wait_tile();
+    __syncthreads();
+    mphase(std::false_type{}, std::true_type{}, 0, (nt - 1) & 3);
+    wait_vmcnt<0>();  // no copy may land after the stages are reused below
+    __syncthreads();
+    if (!grp) __syncthreads();  // first half: match the second's count
   }
 
-  // dQ = scale * dS K (dQ^T accumulated: lane = query row, 4 consecutive d).
-  if (my_m < p.Sq) {
+  // dQ = scale * dS K: the second half's partial dQ^T goes through LDS to the
+  // first half, which adds it (fixed order) and stores.
+  float* xq = (float*)smem + (slot * 64 + lane) * 4;  // 16 B per lane, blocks NS * 1 KB apart
+  if (grp) {
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *(f32x4*)(xq + (4 * db + i) * C::NS * 64 * 4) =
+            f32x4{dq[db][4 * i], dq[db][4 * i + 1], dq[db][4 * i + 2], dq[db][4 * i + 3]};
+  }
+  __syncthreads();
+  if (!grp && my_m < p.Sq) {
     T* out = (T*)a.dq.data + b * a.dq.sb + hq * a.dq.sh + (int64_t)my_m * a.dq.ss + 4 * h;
     const float sc = p.scale;
 #pragma unroll
     for (int db = 0; db < C::DB; ++db)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        st_global8(out + 32 * db + 8 * i, pack4<T>(dq[db][4 * i] * sc, dq[db][4 * i + 1] * sc,
-                                                  dq[db][4 * i + 2] * sc, dq[db][4 * i + 3] * sc));
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 o = *(const f32x4*)(xq + (4 * db + i) * C::NS * 64 * 4);
+        st_global8(out + 32 * db + 8 * i,
+                   pack4<T>((dq[db][4 * i] + o[0]) * sc, (dq[db][4 * i + 1] + o[1]) * sc,
+                            (dq[db][4 * i + 2] + o[2]) * sc, (dq[db][4 * i + 3] + o[3]) * sc));
+      }
   }
 }
 
@@ -385,7 +361,7 @@ hipError_t launch_q(const BwdArgs& a, hipStream_t st) {
   using C = QCfg<D>;
   BwdArgs x = a;
   const int gp = gqa_pack4(a.p.G);
-  const int bmh = 32 * (C::NW / gp);
+  const int bmh = 32 * (C::NS / gp);
   const int nqt = (a.p.Sq + bmh - 1) / bmh;
   x.ntiles = (nqt << 8) | gp;
   const dim3 grid(nqt * (a.p.G / gp) * a.p.B * a.p.Hkv), block(C::NW * 64);
