@@ -52,6 +52,8 @@ struct QCfg {
   static constexpr int E = TILEB / (1024 * NW);   // 1 KB copies per wave per tensor
   static constexpr int STAGEB = 2 * TILEB;
   static constexpr int STAGES = 4;
+  static constexpr int RA = 4;  // row reads issued this many MFMAs ahead
+  static constexpr int RB = 3;  // transpose reads issued this many dQ MFMAs ahead
   static_assert(E * 1024 * NW == TILEB, "tile must split into 1 KB copies");
   static_assert(NS * 64 * 64 * 4 <= STAGES * STAGEB, "the partial-dQ exchange fits in the stage memory");
 };
@@ -245,8 +247,8 @@ void bwd_q_kernel(BwdArgs a) {
 
   // MFMA phase: S^T / dP^T of the tile in stage sk (DO_S) and dQ^T of the
   // previous tile in stage sq with PS (DO_Q): a dQ MFMA after every second
-  // S / dP MFMA.  Row reads are kept four MFMAs ahead, transpose reads two
-  // dQ MFMAs ahead.
+  // S / dP MFMA.  Row reads are kept RA MFMAs ahead, transpose reads RB dQ
+  // MFMAs ahead.
   auto mphase = [&](auto do_s_c, auto do_q_c, int sk, int sq) {
     constexpr bool DO_S = decltype(do_s_c)::value, DO_Q = decltype(do_q_c)::value;
     const char* sK = smem + sk * C::STAGEB;
@@ -260,32 +262,33 @@ void bwd_q_kernel(BwdArgs a) {
       lo = lds_read_tr4(base + voff_lo[db]);
       hi = lds_read_tr4(base + voff_hi[db]);
     };
-    i32x4 ab[5];
-    i16x4 blo[3], bhi[3];
+    constexpr int RA = C::RA, RB = C::RB;
+    i32x4 ab[RA + 1];
+    i16x4 blo[RB + 1], bhi[RB + 1];
     if constexpr (DO_S) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) ab[k] = rdA(k);
+      for (int k = 0; k < RA; ++k) ab[k] = rdA(k);
       S = f32x16{};
       DP = f32x16{};
     }
     if constexpr (DO_Q) {
-      rdB(0, blo[0], bhi[0]);
-      rdB(1, blo[1], bhi[1]);
+#pragma unroll
+      for (int j = 0; j < RB; ++j) rdB(j, blo[j], bhi[j]);
     }
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (DO_S) {
-        if (k + 4 < 16) ab[(k + 4) % 5] = rdA(k + 4);
-        if (k & 1) DP = M::mma(as_v8<V8>(ab[k % 5]), df[k >> 1], DP);
-        else S = M::mma(as_v8<V8>(ab[k % 5]), qf[k >> 1], S);
+        if (k + RA < 16) ab[(k + RA) % (RA + 1)] = rdA(k + RA);
+        if (k & 1) DP = M::mma(as_v8<V8>(ab[k % (RA + 1)]), df[k >> 1], DP);
+        else S = M::mma(as_v8<V8>(ab[k % (RA + 1)]), qf[k >> 1], S);
       }
       if constexpr (DO_Q) {
         if (k & 1) {
           const int j = k >> 1;
-          if (j + 2 < 8) rdB(j + 2, blo[(j + 2) % 3], bhi[(j + 2) % 3]);
+          if (j + RB < 8) rdB(j + RB, blo[(j + RB) % (RB + 1)], bhi[(j + RB) % (RB + 1)]);
           const int db = j % C::DB, c16 = j / C::DB;
-          dq[db] = M::mma(cat_tr<V8>(blo[j % 3], bhi[j % 3]), PS[c16], dq[db]);
+          dq[db] = M::mma(cat_tr<V8>(blo[j % (RB + 1)], bhi[j % (RB + 1)]), PS[c16], dq[db]);
         }
       }
     }
