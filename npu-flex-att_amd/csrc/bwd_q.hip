@@ -110,6 +110,17 @@ void bwd_q_kernel(BwdArgs a) {
     // a row with no allowed key (LSE = -inf) contributes nothing: every one of
     // its pairs is masked, and +inf makes exp2(y - lse2) = 0 for those
     if (!(lse2 > kNegInf)) lse2 = kPosInf;
+    // Wait for these loads here, once: without the pins the compiler places a
+    // vmcnt(0) wait at their first use inside the tile loop, which would also
+    // drain the tile copies in flight on every tile.
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int kc = 0; kc < C::KC; ++kc) {
+      pin(qf[kc]);
+      pin(df[kc]);
+    }
+    pin(lse2);
+    pin(dlt);
   }
   f32x16 dq[C::DB];
 #pragma unroll
