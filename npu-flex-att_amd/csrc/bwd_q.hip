@@ -24,8 +24,9 @@
 //    phase issues the S / dP MFMAs of tile t and the dQ MFMAs of tile t-1
 //    (24 independent MFMAs); a VALU phase forms P and dS of tile t.  While
 //    one wave of a SIMD streams MFMAs the other runs its VALU phase.
-//  * K / V tiles are copied global -> LDS with direct-to-LDS loads three tiles
-//    ahead into four stages; every phase ends with a workgroup barrier.
+//  * K / V tiles are copied global -> LDS with direct-to-LDS loads two tiles
+//    ahead into four stages, issued in the VALU phases; every phase ends with
+//    a workgroup barrier.
 // Deterministic: every output element is owned by one lane pair and
 // accumulated in a fixed order.
 #include "flexatt_device.h"
@@ -310,27 +311,27 @@ void bwd_q_kernel(BwdArgs a) {
     }
   };
 
+  // Copies are issued at the start of a VALU phase (the shorter one): a global
+  // -> LDS copy holds its wave for tens of cycles at issue.  Tile u + 2 goes
+  // to the stage of tile u - 2, whose last reads (dQ of tile u - 2) ended one
+  // phase earlier for both halves.
   if (nt > 0) {
     issue_next();  // t_lo
     issue_next();  // t_lo + 1
     wait_tile();
     __syncthreads();
     if (grp) __syncthreads();  // second half starts one phase late
-    issue_next();  // t_lo + 2
     mphase(std::true_type{}, std::false_type{}, 0, 0);
-    wait_tile();
     __syncthreads();
     for (int u = 0; u + 1 < nt; ++u) {
+      issue_next();  // t_lo + u + 2
       vphase((t_lo + u) * C::BN);
-      wait_tile();
+      wait_tile();  // tile u + 1 landed
       __syncthreads();
-      issue_next();  // t_lo + u + 3
       mphase(std::true_type{}, std::true_type{}, (u + 1) & 3, u & 3);
-      wait_tile();
       __syncthreads();
     }
     vphase((t_hi - 1) * C::BN);
-    wait_tile();
     __syncthreads();
     mphase(std::false_type{}, std::true_type{}, 0, (nt - 1) & 3);
     wait_vmcnt<0>();  // no copy may land after the stages are reused below
