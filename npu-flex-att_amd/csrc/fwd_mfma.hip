@@ -16,9 +16,10 @@
 //    the two wave halves and the O rescale is a per-lane scalar.
 //  * O^T = V^T P^T, with P^T taken straight from the S^T accumulators and V^T
 //    read from the row-major V tile with the LDS transpose read.
-//  * K/V tiles are copied global -> LDS with direct-to-LDS loads into three
-//    stages, two tiles ahead of the tile being computed (no staging
-//    registers, one barrier per tile).  Tiles are unpadded with a per-row
+//  * K/V tiles are copied global -> LDS with direct-to-LDS loads (no staging
+//    registers): into four stages three tiles ahead with the 8-wave
+//    ping-pong (one barrier per phase), into three stages two tiles ahead
+//    with 4 waves (one barrier per tile).  Tiles are unpadded with a per-row
 //    chunk swizzle (swz_col for K, swz_tr for V).
 //  * Lazy rescale: the running max only moves when a row's max grows by more
 //    than 2^8, so O is rescaled rarely; P <= 2^8 stays exact in fp16/bf16 and
