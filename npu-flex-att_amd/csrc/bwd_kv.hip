@@ -30,10 +30,12 @@
 //      M(u): S-wave: the 16 S / dP MFMAs of tile u;  KV-wave: reads the packed
 //            P / dS of tile u-1 and the first transpose reads;
 //      V(u): S-wave: P / dS of tile u (VALU), written to the exchange buffer;
-//            KV-wave: the 16 dV / dK MFMAs of tile u-1 and the copies of tile
-//            u+4, then waits for tile u+1 and converts its LSE to log2 units.
+//            KV-wave: the 16 dV / dK MFMAs of tile u-1, then waits for tile
+//            u+1 and converts its LSE to log2 units;
 //    so that each SIMD alternates between the S-wave's MFMAs and the
-//    KV-wave's MFMAs beside the S-wave's VALU work.
+//    KV-wave's MFMAs beside the S-wave's VALU work.  The KV-wave issues the
+//    copies of tile u+4 in M(u): a global -> LDS copy holds its wave for
+//    tens of cycles at issue, which the MFMA phases cannot afford.
 //  * Q and dO are read two ways from the same tile, as rows (S, dP) and as
 //    columns (dV^T, dK^T, with the LDS transpose read); the dual-use swizzle
 //    keeps both conflict-free.
@@ -361,9 +363,15 @@ void bwd_kv_kernel(BwdArgs a) {
     __syncthreads();  // prologue
     for (int u = 0; u <= ntile; ++u) {
       const bool act = u > 0;
-      // ---- M(u): packed P / dS of tile u-1, first transpose reads ----------
+      // ---- M(u): copies of tile u + AHEAD (a global -> LDS copy holds its
+      //      wave for tens of cycles at issue, so they stay out of the MFMA
+      //      phase), packed P / dS of tile u-1, first transpose reads --------
       V8 PP[2], PS[2];
       i16x4 blo[5], bhi[5];
+      if (ntile > 0) {
+#pragma unroll
+        for (int j = 0; j < CNT; ++j) copy_op(s_cp, j);
+      }
       if (act) {
 #pragma unroll
         for (int db = 0; db < C::DB; ++db) {
@@ -380,13 +388,12 @@ void bwd_kv_kernel(BwdArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();  // X(u)
       __builtin_amdgcn_sched_barrier(0);
-      // ---- V(u): dV / dK of tile u-1, copies of tile u + AHEAD ------------
+      // ---- V(u): dV / dK of tile u-1 ---------------------------------------
       if (act) {
 #pragma unroll
         for (int j = 0; j < 4 * C::DB; ++j) {
           __builtin_amdgcn_sched_barrier(0);
           if (j + 4 < 4 * C::DB) rdB(j + 4, blo[(j + 4) % 5], bhi[(j + 4) % 5]);
-          if (j >= 2 && j < 2 + CNT) copy_op(s_cp, j - 2);
           const int db = (j >> 1) % C::DB, qc = (j >> 1) / C::DB;
           const V8 av = cat_tr<V8>(blo[j % 5], bhi[j % 5]);
           if (j & 1) dk[db] = M::mma(av, PS[qc], dk[db]);
@@ -394,9 +401,6 @@ void bwd_kv_kernel(BwdArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
         s_tr = s_tr + 1 == C::STAGES ? 0 : s_tr + 1;
-      } else if (ntile > 0) {
-#pragma unroll
-        for (int j = 0; j < CNT; ++j) copy_op(s_cp, j);
       }
       if (ntile > 0) {
         advance();
