@@ -274,12 +274,14 @@ void fwd_mfma_kernel(FwdArgs a) {
     // Ping-pong.  Waves 0-3 and 4-7 (one of each on every SIMD) run the same
     // program one phase apart, phases separated by workgroup barriers:
     //   MFMA phase  M(t): S^T(t) = K(t) Q^T and O^T += V^T P(t-1)^T, 32
-    //                     independent MFMAs fed from LDS, with the packing of
-    //                     P(t-1) and its row sums issued in their shadow;
-    //   VALU phase  V(t): mask, row max, rescale, E(t) = exp2(y - m).
+    //                     independent MFMAs fed from LDS, plus the copies of
+    //                     tile t+2;
+    //   VALU phase  V(t): mask, row max, rescale, P(t) = exp2(y - m), its row
+    //                     sums and its packing into PV operands.
     // While one wave of a SIMD is in its MFMA phase the other is in its VALU
-    // phase.  A single wave issues VALU work at well under the SIMD's VALU
-    // rate, so both waves carry part of the softmax work.
+    // phase.  (Moving the packing and row sums into the MFMA phase, or the
+    // copies into the VALU phase, measured slower: the two phases are about
+    // equally long.)
     // Tile u lives in stage (u - t_lo) % 4 from its copy (issued at the start
     // of M(u-2)) until B's M(u+1) has read V(u); the copy of tile u+4 into
     // that stage is issued at M(u+2), after the barrier that ends B's M(u+1).
