@@ -27,11 +27,12 @@
 //    is Q, dO (32 x D each), LSE and Delta (32 floats each), copied global ->
 //    LDS with direct-to-LDS loads four tiles ahead into six stages.
 //  * Step u has two phases separated by workgroup barriers:
-//      M(u): S-wave: the 16 S / dP MFMAs of tile u;  KV-wave: reads the packed
-//            P / dS of tile u-1 and the first transpose reads;
+//      M(u): S-wave: the 16 S / dP MFMAs of tile u, with the reads of its
+//            LSE (converted to log2 units) and Delta;  KV-wave: reads the
+//            packed P / dS of tile u-1 and the first transpose reads;
 //      V(u): S-wave: P / dS of tile u (VALU), written to the exchange buffer;
 //            KV-wave: the 16 dV / dK MFMAs of tile u-1, then waits for tile
-//            u+1 and converts its LSE to log2 units;
+//            u+1;
 //    so that each SIMD alternates between the S-wave's MFMAs and the
 //    KV-wave's MFMAs beside the S-wave's VALU work.  The KV-wave issues the
 //    copies of tile u+4 in M(u): a global -> LDS copy holds its wave for
@@ -157,11 +158,12 @@ void bwd_kv_kernel(BwdArgs a) {
     int cg = 0, cqt = qt_top;  // tile being formed (head, query tile)
     int sc = 0;               // its stage
 
-    __syncthreads();  // prologue: tile 0 landed, its LSE in log2 units
+    __syncthreads();  // prologue: tile 0 landed
     for (int u = 0; u <= ntile; ++u) {
       const bool act = u < ntile;
       f32x16 S, DP;
-      // ---- M(u): S = Q K^T, dP = dO V^T of tile u -------------------------
+      f32x4 L4[4], D4[4];  // LSE (to log2 units) and Delta of this lane's query rows
+      // ---- M(u): S = Q K^T, dP = dO V^T of tile u; LSE / Delta reads ------
       if (act) {
         // Row-read addresses of this stage (the Q / dO choice folds into the
         // instruction offset).
@@ -178,6 +180,19 @@ void bwd_kv_kernel(BwdArgs a) {
         for (int k = 0; k < 2 * C::KC; ++k) {
           __builtin_amdgcn_sched_barrier(0);
           if (k + 4 < 2 * C::KC) ab[(k + 4) % 5] = rdA(k + 4);
+          if (k == 8) {  // query rows m0 + 8i + 4h + j
+            const float* sR = (const float*)(smem + sc * C::STAGEB + 2 * C::TILEB);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              L4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 4 * h));
+              D4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 8 + 4 * h));
+            }
+          }
+          if (k >= 12) {  // LSE -> log2 units
+            const int i = k - 12;
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) L4[i][jj] *= kLog2e;
+          }
           if (k & 1) DP = M::mma(as_v8<V8>(ab[k % 5]), vreg[k >> 1], DP);
           else S = M::mma(as_v8<V8>(ab[k % 5]), kreg[k >> 1], S);
         }
@@ -197,38 +212,43 @@ void bwd_kv_kernel(BwdArgs a) {
           cg = 0;
           --cqt;
         }
-        // LSE (log2 units) and Delta of this lane's query rows m0 + 8i + 4h + j.
-        const float* sR = (const float*)(smem + sc * C::STAGEB + 2 * C::TILEB);
         sc = sc + 1 == C::STAGES ? 0 : sc + 1;
-        f32x4 L4[4], D4[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          L4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 4 * h));
-          D4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 8 + 4 * h));
-        }
-        // Element r is query row m0 + 8(r/4) + 4h + r%4, KV row my_kv.
+        // Element r is query row m0 + 8(r/4) + 4h + r%4, KV row my_kv.  Each
+        // step runs over all 16 elements before the next one starts, so that
+        // no instruction waits on the one just before it.
         auto form = [&](auto masked) {
           f32x16 pe, de;
+          float y[16], tt[16];
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int q = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
-            float t = 0.f, e;
+            tt[r] = 0.f;
             if constexpr (RAW) {
-              e = fast_exp2(__builtin_fmaf(S[r], c2, -L4[r >> 2][r & 3]));
+              y[r] = __builtin_fmaf(S[r], c2, -L4[r >> 2][r & 3]);
             } else {
-              const float y = score_log2<SOFTCAP, ALIBI>(S[r], p, sl, q, my_kv, t);
-              e = fast_exp2(y - L4[r >> 2][r & 3]);
+              const int q = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+              y[r] = score_log2<SOFTCAP, ALIBI>(S[r], p, sl, q, my_kv, tt[r]) - L4[r >> 2][r & 3];
             }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float e = fast_exp2(y[r]);
             if constexpr (decltype(masked)::value) {
+              const int q = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
               const bool ok = (q < p.Sq) & (my_kv < p.Skv) & (!p.causal | (my_kv <= q)) &
                               ((p.window == 0) | (q - my_kv <= p.window));
               e = ok ? e : 0.f;
             }
-            float ds = e * (DP[r] - D4[r >> 2][r & 3]);
-            if constexpr (SOFTCAP) ds *= 1.f - t * t;
             pe[r] = e;
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float ds = pe[r] * (DP[r] - D4[r >> 2][r & 3]);
+            if constexpr (SOFTCAP) ds *= 1.f - tt[r] * tt[r];
             de[r] = ds;
           }
+          __builtin_amdgcn_sched_barrier(0);
           *(V8*)xslot(u, 0) = pack8<T>(pe, 0);
           *(V8*)xslot(u, 1) = pack8<T>(pe, 8);
           *(V8*)xslot(u, 2) = pack8<T>(de, 0);
@@ -330,14 +350,6 @@ void bwd_kv_kernel(BwdArgs a) {
       }
     };
     constexpr int CNT = 2 * C::E + 1;  // copy operations per tile per KV-wave
-    // LSE values of a landed tile -> log2 units, in place: each KV-wave
-    // converts the 8 it copied (the next barrier orders this before the reads).
-    auto lse_to_log2 = [&](int st) {
-      if (lane < 8) {
-        float* sR = (float*)(smem + st * C::STAGEB + 2 * C::TILEB) + 16 * pr + lane;
-        *sR *= kLog2e;
-      }
-    };
     // Transpose reads (A operands of dV^T / dK^T) of MFMA j; tb_lo / tb_hi
     // are the lane addresses in the tile's stage (Q / dO and the 16-row block
     // fold into the instruction offset).
@@ -348,7 +360,7 @@ void bwd_kv_kernel(BwdArgs a) {
       lo = lds_read_tr4(smem + (tb_lo[db] + off));
       hi = lds_read_tr4(smem + (tb_hi[db] + off));
     };
-    int s_tr = 0, s_cp = C::AHEAD % C::STAGES, s_ls = 1;  // stages of tiles u-1, u+AHEAD, u+1
+    int s_tr = 0, s_cp = C::AHEAD % C::STAGES;  // stages of tiles u-1 and u+AHEAD
 
     if (ntile > 0) {
 #pragma unroll
@@ -358,7 +370,6 @@ void bwd_kv_kernel(BwdArgs a) {
         advance();
       }
       wait_vmcnt<(C::AHEAD - 1) * CNT>();
-      lse_to_log2(0);
     }
     __syncthreads();  // prologue
     for (int u = 0; u <= ntile; ++u) {
@@ -405,9 +416,7 @@ void bwd_kv_kernel(BwdArgs a) {
       if (ntile > 0) {
         advance();
         wait_vmcnt<(C::AHEAD - 1) * CNT>();  // tile u+1 landed
-        lse_to_log2(s_ls);
         s_cp = s_cp + 1 == C::STAGES ? 0 : s_cp + 1;
-        s_ls = s_ls + 1 == C::STAGES ? 0 : s_ls + 1;
       }
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();  // Y(u)
