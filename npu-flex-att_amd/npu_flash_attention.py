@@ -138,23 +138,28 @@ def npu_flash_attention_forward(
     if not _kernel_ready(O):
         O = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     LSE = torch.empty(B, Hq, Sq, device=query.device, dtype=torch.float32)
-    if O.numel() == 0 or Sk == 0:
+    _forward_into(query, key, value, O, LSE, causal=causal, sliding_window=sliding_window,
+                  alibi=alibi_slope, scale=scale, soft_cap=soft_cap)
+    if return_lse:
+        return O, LSE
+    return O
+
+
+def _forward_into(query, key, value, O, LSE, *, causal, sliding_window, alibi, scale, soft_cap):
+    """Run the forward kernels into the caller's ``O`` (kernel-ready layout)
+    and contiguous fp32 ``LSE``; shapes are already validated."""
+    if O.numel() == 0 or key.shape[2] == 0:
         O.zero_()
         LSE.fill_(float("-inf"))
-        return (O, LSE) if return_lse else O
-
+        return
     lib = _lib.load()
     q, k, v = _prepare(query), _prepare(key), _prepare(value)
-    slopes = _alibi(alibi_slope, Hq, query.device)
+    slopes = _alibi(alibi, query.shape[1], query.device)
     p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes)
     with torch.cuda.device(query.device):
         st = lib.flexatt_fwd(p, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v), _lib.tensor(O),
                              LSE.data_ptr(), _stream(query.device))
     _lib.check(st, "flexatt_fwd")
-
-    if return_lse:
-        return O, LSE
-    return O
 
 
 # ------------------------------------------------------------ backward (L2) --
@@ -196,22 +201,33 @@ def npu_flash_attention_backward(
         DQ = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     DK = torch.empty(B, Hkv, Sk, D, device=key.device, dtype=key.dtype)
     DV = torch.empty(B, Hkv, Sk, D, device=value.device, dtype=value.dtype)
-    if DQ.numel() == 0 or DK.numel() == 0:
-        return DQ.zero_(), DK.zero_(), DV.zero_()
-    delta = torch.empty(B, Hq, Sq, device=query.device, dtype=torch.float32)
+    _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, causal=causal,
+                   sliding_window=sliding_window, alibi=alibi_slope, scale=scale, soft_cap=soft_cap)
+    return DQ, DK, DV
 
+
+def _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, *, causal, sliding_window,
+                   alibi, scale, soft_cap):
+    """Run Delta, dQ and dK/dV into the caller's ``DQ`` (kernel-ready layout)
+    and contiguous ``DK`` / ``DV``; shapes are already validated."""
+    if DQ.numel() == 0 or DK.numel() == 0:
+        DQ.zero_()
+        DK.zero_()
+        DV.zero_()
+        return
+    B, Hq, Sq, _ = query.shape
+    delta = torch.empty(B, Hq, Sq, device=query.device, dtype=torch.float32)
     lib = _lib.load()
     q, k, v = _prepare(query), _prepare(key), _prepare(value)
     o, do = _prepare(out), _prepare(grad_out)
     lse = lse.to(torch.float32).contiguous()
-    slopes = _alibi(alibi_slope, Hq, query.device)
+    slopes = _alibi(alibi, Hq, query.device)
     p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes)
     with torch.cuda.device(query.device):
         st = lib.flexatt_bwd(p, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v), _lib.tensor(o),
                              _lib.tensor(do), lse.data_ptr(), delta.data_ptr(), _lib.tensor(DQ),
                              _lib.tensor(DK), _lib.tensor(DV), _stream(query.device))
     _lib.check(st, "flexatt_bwd")
-    return DQ, DK, DV
 
 
 # ----------------------------------------------------------- autograd (L3) --
