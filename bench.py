@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--config", default="gqa_llama3_8b", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bounded CPU baseline sample budget")
+    ap.add_argument("--layout", default="bnsd", choices=("bnsd", "bsnd"),
+                    help="storage of Q/K/V/dO (and so O, dQ, dK, dV): [B,H,S,D], or [B,S,H,D] passed as strided views")
+    ap.add_argument("--no-gemm-peak", action="store_true", help="skip the plain bf16 GEMM reference rate")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one 256 MiB device copy (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -107,6 +110,8 @@ def main():
     k = (torch.randn(B, Hkv, Skv, D, generator=g) * insc).to(dtype).to(dev)
     v = (torch.randn(B, Hkv, Skv, D, generator=g) * insc).to(dtype).to(dev)
     do = torch.randn(B, Hq, Sq, D, generator=g).to(dtype).to(dev)
+    if args.layout == "bsnd":  # same values, [B, S, H, D] storage, viewed as [B, H, S, D]
+        q, k, v, do = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v, do))
     slopes = None
     if alibi:
         slopes = torch.tensor([2.0 ** (-8.0 * (h + 1) / Hq) for h in range(Hq)], dtype=torch.float32, device=dev)
@@ -180,6 +185,8 @@ def main():
     dom = max(per_kernel_flop, key=lambda n: kernel_ms[n])
     achieved = per_kernel_flop[dom] / kernel_ms[dom] / 1e9
 
+    gemm = None if args.no_gemm_peak else gemm_peak(dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(q, k, v, do, kw, slopes, args.cpu_seconds, Hq // Hkv, causal, window, D, Sq, Skv)
@@ -201,7 +208,7 @@ def main():
             "workload": f"{args.config}: {dts} B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} Skv={Skv} D={D} causal={causal} "
                         f"window={window} soft_cap={cap} alibi={alibi} scale={scale}; step = fwd + bwd",
             "batch": B, "heads_q": Hq, "heads_kv": Hkv, "seqlen_q": Sq, "seqlen_kv": Skv, "head_dim": D,
-            "parallelism": "single GPU",
+            "parallelism": "single GPU", "layout": args.layout,
         },
         "fwd_ms": round(fwd_ms, 4),
         "bwd_ms": round(bwd_ms, 4),
@@ -222,7 +229,31 @@ def main():
         },
         "cpu_baseline": cpu,
     }
+    if gemm is not None:
+        # secondary denominator: what a plain library bf16 GEMM reaches on this GPU
+        out["gemm_peak"] = gemm
+        out["frac_gemm_peak"] = round(total_tf / gemm["tflops"], 4)
     print(json.dumps(out), flush=True)
+
+
+def gemm_peak(dev):
+    """Plain bf16 GEMM rate (torch.matmul, i.e. hipBLASLt): 8192^3, median of 20."""
+    import torch
+
+    n = 8192
+    a = torch.randn(n, n, device=dev).to(torch.bfloat16)
+    b = torch.randn(n, n, device=dev).to(torch.bfloat16)
+    for _ in range(3):
+        torch.matmul(a, b)
+    st = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
+    for e0, e1 in evs:
+        e0.record(st)
+        torch.matmul(a, b)
+        e1.record(st)
+    torch.cuda.synchronize()
+    ms = statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+    return {"tflops": round(2.0 * n ** 3 / ms / 1e9, 1), "shape": f"{n}x{n}x{n} bf16 torch.matmul"}
 
 
 def cpu_baseline(q, k, v, do, kw, slopes, budget_s, G, causal, window, D, Sq, Skv):
