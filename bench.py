@@ -38,6 +38,13 @@ CONFIGS = {
     "all_primitives_d64": (1, 28, 4, 16384, 16383, 64, "fp16", True, 2048, 30.0, True, 0.05, 1.0),
     "mha_d64_s2048": (1, 2, 2, 2048, 2048, 64, "fp16", True, 0, 0.0, False, None, 1.0),
 }
+# Decoding workloads (forward only, split-KV kernels): one new token per
+# sequence against a KV cache; HBM-bound, reported in GB/s of K + V read.
+DECODE_CONFIGS = {
+    "decode_llama3_8b_32k": (8, 32, 8, 1, 32768, 128, "bf16", False, 0, 0.0, False, None, 1.0),
+    "decode_gqa_d64_16k": (4, 28, 4, 4, 16384, 64, "fp16", False, 0, 0.0, False, None, 1.0),
+}
+HBM_PEAK_GBS = 8000.0
 
 
 def parse():
@@ -45,7 +52,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="gqa_llama3_8b", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="gqa_llama3_8b", choices=sorted(CONFIGS) + sorted(DECODE_CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bounded CPU baseline sample budget")
     ap.add_argument("--layout", default="bnsd", choices=("bnsd", "bsnd"),
@@ -103,6 +110,8 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.config in DECODE_CONFIGS:
+        return decode_main(args, dev)
     B, Hq, Hkv, Sq, Skv, D, dts, causal, window, cap, alibi, scale, insc = CONFIGS[args.config]
     dtype = {"bf16": torch.bfloat16, "fp16": torch.float16}[dts]
     g = torch.Generator().manual_seed(42)
@@ -233,6 +242,99 @@ def main():
         # secondary denominator: what a plain library bf16 GEMM reaches on this GPU
         out["gemm_peak"] = gemm
         out["frac_gemm_peak"] = round(total_tf / gemm["tflops"], 4)
+    print(json.dumps(out), flush=True)
+
+
+def decode_main(args, dev):
+    """Decoding step (forward only) through the drop-in forward, which takes
+    the split-KV kernels for this shape; value = K + V bytes / step time."""
+    import torch
+
+    import flexatt_lib as L
+    import npu_flash_attention as nfa
+
+    B, Hq, Hkv, Sq, Skv, D, dts, causal, window, cap, alibi, scale, insc = DECODE_CONFIGS[args.config]
+    dtype = {"bf16": torch.bfloat16, "fp16": torch.float16}[dts]
+    g = torch.Generator().manual_seed(42)
+    q = torch.randn(B, Hq, Sq, D, generator=g).to(dtype).to(dev)
+    k = torch.randn(B, Hkv, Skv, D, generator=g).to(dtype).to(dev)
+    v = torch.randn(B, Hkv, Skv, D, generator=g).to(dtype).to(dev)
+    kw = dict(causal=causal, sliding_window=window, soft_cap=cap, scale=scale)
+    p = nfa._problem(q, k, scale if scale is not None else 1.0 / math.sqrt(D), causal, window, cap, None)
+    assert L.load().flexatt_fwd_decode_workspace(p) > 0, "workload outside the decode kernels' range"
+    st = torch.cuda.current_stream(dev)
+
+    def timed(n):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        for e0, e1 in evs:
+            e0.record(st)
+            nfa.npu_flash_attention_forward(q, k, v, return_lse=True, **kw)
+            e1.record(st)
+        torch.cuda.synchronize()
+        return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+
+    for _ in range(args.warmup):
+        nfa.npu_flash_attention_forward(q, k, v, return_lse=True, **kw)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        nfa.npu_flash_attention_forward(q, k, v, return_lse=True, **kw)
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms_ev = timed(max(args.steps, 10))
+    nfa.decode_enabled = False  # the regular forward kernel on the same step, for reference
+    try:
+        for _ in range(3):
+            nfa.npu_flash_attention_forward(q, k, v, return_lse=True, **kw)
+        ms_regular = timed(max(args.steps, 10))
+    finally:
+        nfa.decode_enabled = True
+    es = q.element_size()
+    kv_bytes = 2 * B * Hkv * Skv * D * es
+    io_bytes = kv_bytes + 2 * B * Hq * Sq * D * es + B * Hq * Sq * 4
+    gbs = kv_bytes / ms_step / 1e6
+    achieved = io_bytes / ms_ev / 1e6
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import attention_oracle as orc
+
+        torch.set_num_threads(os.cpu_count() or 1)
+        G = Hq // Hkv
+        qc, kc, vc = (t.float().cpu() for t in (q, k, v))
+        done, t1 = 0, time.perf_counter()
+        for b in range(B):
+            for h in range(Hkv):
+                orc.forward(qc[b:b + 1, h * G:(h + 1) * G], kc[b:b + 1, h:h + 1], vc[b:b + 1, h:h + 1], causal,
+                            window, None, kw["scale"], cap, torch.float32)
+                done += 1
+            if time.perf_counter() - t1 > args.cpu_seconds:
+                break
+        secs = time.perf_counter() - t1
+        cpu = {"value": round(2 * done * Skv * D * es / secs / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+               "kind": "port", "sample": f"{done} of {B * Hkv} (batch, KV-head) groups, fp32 eager oracle forward, "
+                                         f"{secs:.1f} s"}
+    out = {
+        "metric": "decode attention K+V HBM throughput (split-KV forward)",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dts,
+        "data": "synthetic N(0,1), seed 42, resident in HBM",
+        "config": {"workload": f"{args.config}: {dts} B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} Skv={Skv} D={D} "
+                               f"causal={causal}; step = one forward (O, LSE)",
+                   "batch": B, "heads_q": Hq, "heads_kv": Hkv, "seqlen_q": Sq, "seqlen_kv": Skv, "head_dim": D,
+                   "parallelism": "single GPU"},
+        "kernel_ms": {"decode_and_merge": round(ms_ev, 4), "regular_forward": round(ms_regular, 4)},
+        "roofline": {"kernel": "decode", "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
     print(json.dumps(out), flush=True)
 
 

@@ -28,6 +28,7 @@
 #ifndef FLEXATT_H_
 #define FLEXATT_H_
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -44,7 +45,8 @@ enum flexatt_status {
   FLEXATT_EDTYPE = -2,     /* unknown dtype */
   FLEXATT_EHEADDIM = -3,   /* head_dim not in {32, 64, 128, 256} */
   FLEXATT_ESHAPE = -4,     /* heads_q % heads_kv != 0, or sizes overflow */
-  FLEXATT_ELAYOUT = -5     /* innermost stride != 1 or a row not 16-byte aligned */
+  FLEXATT_ELAYOUT = -5,    /* innermost stride != 1 or a row not 16-byte aligned */
+  FLEXATT_ERANGE = -6      /* problem outside an entry point's range (see its comment) */
 };
 
 /* One [B, H, S, D] tensor: device pointer and element strides. */
@@ -77,6 +79,22 @@ typedef struct flexatt_problem {
  * npu_flash_attention.py:634-652. */
 int flexatt_fwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
                 const flexatt_tensor* v, const flexatt_tensor* o, float* lse, void* stream);
+
+/* Split-KV decode forward (flash-decoding): the results of flexatt_fwd for
+ * problems with few query rows per KV head, computed by splitting the KV
+ * range over many workgroups.  Range: fp16/bf16, head_dim <= 128 and
+ * (heads_q / heads_kv) * seqlen_q <= 32; otherwise FLEXATT_ERANGE.
+ * `workspace` is caller-owned device memory of at least
+ * flexatt_fwd_decode_workspace(p) bytes, 16-byte aligned; it holds partial
+ * results between the two kernels of this call and may be reused once the
+ * call's work on `stream` is done.  Same o / lse as flexatt_fwd up to the
+ * rounding of a different summation order; bitwise deterministic.
+ * Replaces the unused split-KV pair flash_attn_fwd_split_kv_kernel /
+ * flash_attn_fwd_reduce_kernel, npu_flash_attention.py:169-293. */
+size_t flexatt_fwd_decode_workspace(const flexatt_problem* p); /* 0: outside the range */
+int flexatt_fwd_decode(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                       const flexatt_tensor* v, const flexatt_tensor* o, float* lse, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* Backward pre-pass: delta[b,h,i] = sum_d o * dout in fp32.
  * Replaces the torch op at npu_flash_attention.py:681-685. */
@@ -111,7 +129,7 @@ const char* flexatt_status_string(int status);
 /* ABI version of this header (bumped on any signature change). */
 int flexatt_abi_version(void);
 
-#define FLEXATT_ABI_VERSION 1
+#define FLEXATT_ABI_VERSION 2
 
 #ifdef __cplusplus
 }

@@ -93,6 +93,42 @@ const BwdLauncher kDkdv[3][4] = {
     {bwd_dkdv_mfma_bf16_d32, bwd_dkdv_mfma_bf16_d64, bwd_kv_bf16_d128, bwd_dkdv_mfma_bf16_d256},
 };
 
+// Split-KV decode: range, plan and workspace.
+constexpr int kDecWaves = 4;   // waves per workgroup
+constexpr int kDecTile = 32;   // KV rows per tile
+bool decode_applies(const flexatt_problem* p) {
+  return (p->dtype == FLEXATT_F16 || p->dtype == FLEXATT_BF16) && p->head_dim <= 128 &&
+         (int64_t)(p->heads_q / p->heads_kv) * p->seqlen_q <= 32;
+}
+struct DecodePlan {
+  int nsplit, chunk, ntiles;
+  size_t bytes;  // workspace: partial O then partial LSE
+};
+DecodePlan decode_plan(const flexatt_problem* p) {
+  DecodePlan d;
+  // attended KV range: with top-left causal alignment no query row sees past Sq - 1
+  const int kv_hi = p->causal ? (p->seqlen_kv < p->seqlen_q ? p->seqlen_kv : p->seqlen_q) : p->seqlen_kv;
+  d.ntiles = (kv_hi + kDecTile - 1) / kDecTile;
+  // about two workgroups per CU (256 CUs), but at least two tiles per wave
+  const int64_t groups = (int64_t)p->batch * p->heads_kv;
+  int64_t ns = (512 + groups - 1) / groups;
+  const int64_t most = d.ntiles / (2 * kDecWaves);
+  if (ns > most) ns = most;
+  if (ns > 256) ns = 256;
+  if (ns < 1) ns = 1;
+  d.chunk = (int)((d.ntiles + ns - 1) / ns);
+  d.nsplit = (d.ntiles + d.chunk - 1) / d.chunk;  // no workgroup without tiles
+  const int64_t rows = (int64_t)p->batch * p->heads_q * p->seqlen_q;
+  const int64_t parts = d.nsplit;  // one partial per workgroup
+  d.bytes = (size_t)(rows * parts * (p->head_dim + 1) * (int64_t)sizeof(float));
+  return d;
+}
+const DecodeLauncher kDecode[3][3] = {
+    {nullptr, nullptr, nullptr},
+    {fwd_decode_f16_d32, fwd_decode_f16_d64, fwd_decode_f16_d128},
+    {fwd_decode_bf16_d32, fwd_decode_bf16_d64, fwd_decode_bf16_d128},
+};
+
 #define FLEXATT_TRY(x)             \
   do {                             \
     const int rc_ = (x);           \
@@ -133,6 +169,7 @@ const char* flexatt_status_string(int status) {
     case FLEXATT_EHEADDIM: return "unsupported head_dim (expected 32, 64, 128 or 256)";
     case FLEXATT_ESHAPE: return "inconsistent shape (heads_q % heads_kv != 0 or sizes overflow)";
     case FLEXATT_ELAYOUT: return "unsupported layout (innermost stride != 1 or rows not 16-byte aligned)";
+    case FLEXATT_ERANGE: return "problem outside the entry point's range";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown flexatt status";
   }
 }
@@ -154,6 +191,41 @@ int flexatt_fwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
   a.p = make_shape(p);
   a.nqt = 0;
   return (int)kFwd[p->dtype][head_index(p->head_dim)](a, (hipStream_t)stream);
+}
+
+size_t flexatt_fwd_decode_workspace(const flexatt_problem* p) {
+  if (check_problem(p) != FLEXATT_OK || !decode_applies(p)) return 0;
+  return decode_plan(p).bytes;
+}
+
+int flexatt_fwd_decode(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                       const flexatt_tensor* v, const flexatt_tensor* o, float* lse, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  FLEXATT_TRY(check_problem(p));
+  FLEXATT_TRY(check_tensor(q, p->dtype));
+  FLEXATT_TRY(check_tensor(k, p->dtype));
+  FLEXATT_TRY(check_tensor(v, p->dtype));
+  FLEXATT_TRY(check_tensor(o, p->dtype));
+  if (!lse || !workspace) return FLEXATT_EINVAL;
+  if (!decode_applies(p)) return FLEXATT_ERANGE;
+  const DecodePlan d = decode_plan(p);
+  if (workspace_bytes < d.bytes) return FLEXATT_EINVAL;
+  if (((uintptr_t)workspace) % 16 != 0) return FLEXATT_ELAYOUT;
+  DecodeArgs a;
+  a.q = view(q);
+  a.k = view(k);
+  a.v = view(v);
+  a.o = mview(o);
+  a.lse = lse;
+  a.p = make_shape(p);
+  a.nsplit = d.nsplit;
+  a.chunk = d.chunk;
+  a.ntiles = d.ntiles;
+  const int64_t rows = (int64_t)p->batch * p->heads_q * p->seqlen_q;
+  a.part_o = (float*)workspace;
+  a.part_lse = a.part_o + rows * d.nsplit * p->head_dim;
+  if (d.ntiles == 0) return FLEXATT_EINVAL;
+  return (int)kDecode[p->dtype][head_index(p->head_dim)](a, (hipStream_t)stream);
 }
 
 int flexatt_bwd_delta(const flexatt_problem* p, const flexatt_tensor* o, const flexatt_tensor* dout,

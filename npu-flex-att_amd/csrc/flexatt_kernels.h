@@ -30,7 +30,21 @@ struct BwdArgs {
   int ntiles;  // number of row tiles of the kernel's grid (set by the launcher)
 };
 
+// Split-KV decode forward (fwd_decode.hip): partials in the caller's workspace.
+struct DecodeArgs {
+  View q, k, v;
+  MutView o;
+  float* lse;
+  float* part_o;    // [B * Hq * Sq][nsplit][D], O of each partial / its row sums
+  float* part_lse;  // [B * Hq * Sq][nsplit], LSE of each partial in log2 units
+  Shape p;
+  int nsplit;  // workgroups per (b, hkv)
+  int chunk;   // 32-row KV tiles per workgroup
+  int ntiles;  // 32-row KV tiles in the attended range
+};
+
 typedef hipError_t (*FwdLauncher)(const FwdArgs&, hipStream_t);
+typedef hipError_t (*DecodeLauncher)(const DecodeArgs&, hipStream_t);
 typedef hipError_t (*BwdLauncher)(const BwdArgs&, hipStream_t);
 
 #define FLEXATT_DECL_D(D)                                                     \
@@ -51,6 +65,14 @@ FLEXATT_DECL_D(256)
 #undef FLEXATT_DECL_D
 
 hipError_t bwd_delta(int dtype, const DeltaArgs&, hipStream_t);
+
+// Split-KV decode forward (fwd_decode.hip), D <= 128.
+hipError_t fwd_decode_bf16_d32(const DecodeArgs&, hipStream_t);
+hipError_t fwd_decode_f16_d32(const DecodeArgs&, hipStream_t);
+hipError_t fwd_decode_bf16_d64(const DecodeArgs&, hipStream_t);
+hipError_t fwd_decode_f16_d64(const DecodeArgs&, hipStream_t);
+hipError_t fwd_decode_bf16_d128(const DecodeArgs&, hipStream_t);
+hipError_t fwd_decode_f16_d128(const DecodeArgs&, hipStream_t);
 
 // dK/dV as a KV-stationary tile stream (bwd_kv.hip), D = 128.
 hipError_t bwd_kv_bf16_d128(const BwdArgs&, hipStream_t);

@@ -17,6 +17,8 @@ F32, F16, BF16 = 0, 1, 2
 # Entry points declared in include/flexatt.h.
 EXPORTS = (
     "flexatt_fwd",
+    "flexatt_fwd_decode_workspace",
+    "flexatt_fwd_decode",
     "flexatt_bwd_delta",
     "flexatt_bwd_dq",
     "flexatt_bwd_dkdv",
@@ -24,7 +26,7 @@ EXPORTS = (
     "flexatt_status_string",
     "flexatt_abi_version",
 )
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class Tensor(ctypes.Structure):
@@ -81,6 +83,7 @@ def load() -> ctypes.CDLL:
     st = ctypes.c_void_p
     sig = {
         "flexatt_fwd": [pr, T, T, T, T, fp, st],
+        "flexatt_fwd_decode": [pr, T, T, T, T, fp, fp, ctypes.c_size_t, st],
         "flexatt_bwd_delta": [pr, T, T, fp, st],
         "flexatt_bwd_dq": [pr, T, T, T, T, fp, fp, T, st],
         "flexatt_bwd_dkdv": [pr, T, T, T, T, fp, fp, T, T, st],
@@ -90,6 +93,8 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = ctypes.c_int
+    lib.flexatt_fwd_decode_workspace.argtypes = [pr]
+    lib.flexatt_fwd_decode_workspace.restype = ctypes.c_size_t
     lib.flexatt_status_string.argtypes = [ctypes.c_int]
     lib.flexatt_status_string.restype = ctypes.c_char_p
     lib.flexatt_abi_version.argtypes = []

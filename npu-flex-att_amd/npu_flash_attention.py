@@ -40,6 +40,11 @@ __all__ = [
 ]
 
 _DTYPES = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
+
+# The forward takes the split-KV decode kernels (flexatt_fwd_decode) whenever
+# the problem is in their range: fp16/bf16, D <= 128 and (Hq / Hkv) * Sq <= 32.
+# Set to False to force the regular forward kernel (tests compare the two).
+decode_enabled = True
 _HEAD_DIMS = (32, 64, 128, 256)
 
 
@@ -156,7 +161,16 @@ def _forward_into(query, key, value, O, LSE, *, causal, sliding_window, alibi, s
     q, k, v = _prepare(query), _prepare(key), _prepare(value)
     slopes = _alibi(alibi, query.shape[1], query.device)
     p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes)
+    # Few query rows per KV head (decoding): the split-KV kernels, with their
+    # partial results in a workspace from torch's caching allocator.
+    ws_bytes = lib.flexatt_fwd_decode_workspace(p) if decode_enabled else 0
     with torch.cuda.device(query.device):
+        if ws_bytes:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+            st = lib.flexatt_fwd_decode(p, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v), _lib.tensor(O),
+                                        LSE.data_ptr(), ws.data_ptr(), ws_bytes, _stream(query.device))
+            _lib.check(st, "flexatt_fwd_decode")
+            return
         st = lib.flexatt_fwd(p, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v), _lib.tensor(O),
                              LSE.data_ptr(), _stream(query.device))
     _lib.check(st, "flexatt_fwd")

@@ -15,7 +15,7 @@ HEADER = os.path.join(ROOT, "include", "flexatt.h")
 
 def declared_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(flexatt_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(flexatt_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_the_binding_exports():
@@ -31,8 +31,8 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_status_strings():
     lib = L.load()
     assert lib.flexatt_abi_version() == L.ABI_VERSION
-    assert b"#define FLEXATT_ABI_VERSION 1" in open(HEADER, "rb").read()
-    for code in (0, -1, -2, -3, -4, -5):
+    assert b"#define FLEXATT_ABI_VERSION 2" in open(HEADER, "rb").read()
+    for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.flexatt_status_string(code)
     assert b"head_dim" in lib.flexatt_status_string(-3)
 
@@ -100,3 +100,34 @@ def test_null_pointers_rejected():
     assert lib.flexatt_fwd(p, t, t, t, t, None, None) == -1
     assert lib.flexatt_bwd_delta(p, t, t, None, None) == -1
     assert lib.flexatt_fwd(p, tens(data=0), t, t, t, FAKE, None) == -1
+
+
+def test_decode_workspace_range():
+    """flexatt_fwd_decode_workspace: 0 outside the decode range (fp32, D = 256,
+    (Hq / Hkv) * Sq > 32, invalid problem); in range, the bytes of the partials."""
+    lib = L.load()
+    ws = lib.flexatt_fwd_decode_workspace
+    assert ws(problem(dtype=L.F32, seqlen_q=1)) == 0
+    assert ws(problem(head_dim=256, seqlen_q=1)) == 0
+    assert ws(problem(heads_q=8, heads_kv=1, seqlen_q=5)) == 0  # 40 query rows per KV head
+    assert ws(problem(seqlen_q=1, heads_q=3)) == 0              # Hq % Hkv != 0
+    # B=1, Hq=4, Hkv=2, Sq=1, Skv=8192, D=64, not causal: 256 tiles of 32 rows,
+    # splits = min(512 / 2, 256 / 8) = 32, one partial (D + 1 floats) per split and row
+    n = ws(problem(seqlen_q=1, seqlen_kv=8192, causal=0))
+    assert n == 4 * 32 * 65 * 4
+    # causal (top-left): a single query row only ever sees key 0
+    assert ws(problem(seqlen_q=1, seqlen_kv=8192, causal=1)) == 4 * 1 * 65 * 4
+
+
+def test_decode_rejections():
+    lib = L.load()
+    t = tens()
+    p = problem(seqlen_q=1, seqlen_kv=8192, causal=0)
+    need = lib.flexatt_fwd_decode_workspace(p)
+    assert lib.flexatt_fwd_decode(problem(head_dim=256, seqlen_q=1), t, t, t, t, FAKE, FAKE, need, None) == -6
+    assert lib.flexatt_fwd_decode(problem(seqlen_q=64), t, t, t, t, FAKE, FAKE, need, None) == -6
+    assert lib.flexatt_fwd_decode(p, t, t, t, t, FAKE, FAKE, need - 1, None) == -1
+    assert lib.flexatt_fwd_decode(p, t, t, t, t, FAKE, None, need, None) == -1
+    assert lib.flexatt_fwd_decode(p, t, t, t, t, None, FAKE, need, None) == -1
+    assert lib.flexatt_fwd_decode(p, t, t, t, t, FAKE, FAKE + 8, need, None) == -5
+    assert lib.flexatt_fwd_decode(p, t, t, t, tens(stride_d=2), FAKE, FAKE, need, None) == -5
