@@ -72,6 +72,12 @@ typedef struct flexatt_problem {
   int32_t sliding_window; /* W > 0: keep i - j <= W; 0: off */
   float soft_cap;         /* c > 0: x -> c * tanh(x / c); 0: off */
   const float* alibi_slopes; /* device fp32 [Hq]: x += slope[h] * (i - j); NULL: off */
+  /* Document mask (no counterpart in the reference, which lists document
+   * masking as future work, README.md:219): device int32 [B, S, 2] holding,
+   * for position s of batch b, the range [lo, hi) of positions of its
+   * document; i and j attend to each other only inside one document, on top
+   * of the other primitives.  Needs seqlen_q == seqlen_kv = S.  NULL: off. */
+  const int32_t* doc_bounds;
 } flexatt_problem;
 
 /* Forward: o = softmax(mask(score(q k^T))) v and lse.
@@ -129,7 +135,7 @@ const char* flexatt_status_string(int status);
 /* ABI version of this header (bumped on any signature change). */
 int flexatt_abi_version(void);
 
-#define FLEXATT_ABI_VERSION 2
+#define FLEXATT_ABI_VERSION 3
 
 #ifdef __cplusplus
 }

@@ -103,6 +103,19 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(BwdArgs a) {
   int kv_lo = 0, kv_hi = p.Skv;
   if (p.causal) kv_hi = min(kv_hi, m0 + C::BM);
   if (p.window > 0) kv_lo = max(0, m0 - p.window);
+  // document masks: this lane's bounds, the KV range of the workgroup's and
+  // of this wave's rows
+  int dlo, dhi, wlo = 0, whi = 0x7fffffff;
+  doc_bounds(p, b, min(my_m, p.Sq - 1), dlo, dhi);
+  if (p.doc) {
+    int l0, h0, l1, h1;
+    doc_bounds(p, b, min(m0, p.Sq - 1), l0, h0);
+    doc_bounds(p, b, min(m0 + C::BM, p.Sq) - 1, l1, h1);
+    kv_lo = max(kv_lo, l0);
+    kv_hi = min(kv_hi, h1);
+    doc_bounds(p, b, min(mw, p.Sq - 1), wlo, h0);
+    doc_bounds(p, b, min(mw + 31, p.Sq - 1), l1, whi);
+  }
   const int t_lo = kv_lo / C::BN;
   const int t_hi = (kv_hi + C::BN - 1) / C::BN;
 
@@ -146,10 +159,11 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(BwdArgs a) {
     if (C::PREFETCH && t + 1 < t_hi) gload(t + 1);
 
     const int n0 = t * C::BN;
-    const bool skip = (p.causal && n0 > mw + 31) || (p.window > 0 && mw - (n0 + C::BN - 1) > p.window);
+    const bool skip = (p.causal && n0 > mw + 31) || (p.window > 0 && mw - (n0 + C::BN - 1) > p.window) ||
+                      n0 >= whi || n0 + C::BN <= wlo;
     if (skip) continue;
     const bool full = (n0 + C::BN <= p.Skv) && (!p.causal || n0 + C::BN - 1 <= mw) &&
-                      (p.window == 0 || mw + 31 - n0 <= p.window);
+                      (p.window == 0 || mw + 31 - n0 <= p.window) && !p.doc;
 
     f32x16 s[2], dp[2];
 #pragma unroll
@@ -172,7 +186,7 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(BwdArgs a) {
         float tv = 0.f;
         const float y = score_log2<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2, my_m, j, tv);
         float pr = fast_exp2(y - lse2);
-        if (!full && !allowed(p, my_m, j)) pr = 0.f;
+        if (!full && (!allowed(p, my_m, j) || j < dlo || j >= dhi)) pr = 0.f;
         float ds = pr * (dp[bb][r] - dl) * p.scale;
         if constexpr (SOFTCAP) ds *= (1.0f - tv * tv);
         s[bb][r] = ds;
@@ -253,6 +267,19 @@ __global__ __launch_bounds__(256) void bwd_dkdv_mfma_kernel(BwdArgs a) {
   int q_lo = p.causal ? n0 : 0;
   int q_hi = p.Sq;
   if (p.window > 0) q_hi = min(q_hi, n0 + C::BNK + p.window);
+  // document masks (symmetric): the query range of this lane's KV row, of
+  // the workgroup's and of this wave's KV rows
+  int dlo, dhi, wlo = 0, whi = 0x7fffffff;
+  doc_bounds(p, b, min(my_n, p.Skv - 1), dlo, dhi);
+  if (p.doc) {
+    int l0, h0, l1, h1;
+    doc_bounds(p, b, min(n0, p.Skv - 1), l0, h0);
+    doc_bounds(p, b, min(n0 + C::BNK, p.Skv) - 1, l1, h1);
+    q_lo = max(q_lo, l0);
+    q_hi = min(q_hi, h1);
+    doc_bounds(p, b, min(nw, p.Skv - 1), wlo, h0);
+    doc_bounds(p, b, min(nw + 31, p.Skv - 1), l1, whi);
+  }
   const int qt_lo = q_lo / C::BMQ;
   const int qt_hi = (q_hi + C::BMQ - 1) / C::BMQ;
   const int nq = max(0, qt_hi - qt_lo);
@@ -322,9 +349,11 @@ __global__ __launch_bounds__(256) void bwd_dkdv_mfma_kernel(BwdArgs a) {
     const int g = it / nq;
     const int hq = hk * p.G + g;
     const int mt = (qt_lo + it % nq) * C::BMQ;
-    const bool skip = (p.causal && mt + C::BMQ - 1 < nw) || (p.window > 0 && mt - (nw + 31) > p.window);
+    const bool skip = (p.causal && mt + C::BMQ - 1 < nw) || (p.window > 0 && mt - (nw + 31) > p.window) ||
+                      mt >= whi || mt + C::BMQ <= wlo;
     if (skip) continue;
-    const bool full = (!p.causal || mt >= nw + 31) && (p.window == 0 || mt + C::BMQ - 1 - nw <= p.window);
+    const bool full = (!p.causal || mt >= nw + 31) && (p.window == 0 || mt + C::BMQ - 1 - nw <= p.window) &&
+                      !p.doc;
     const float slope_log2 = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
     const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
@@ -350,7 +379,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_mfma_kernel(BwdArgs a) {
           float tv = 0.f;
           const float y = score_log2<SOFTCAP, ALIBI>(s[r], p, slope_log2, m, my_n, tv);
           float pr = fast_exp2(y - L[j]);
-          if (!full && !allowed(p, m, my_n)) pr = 0.f;
+          if (!full && (!allowed(p, m, my_n) || m < dlo || m >= dhi)) pr = 0.f;
           float ds = pr * (dp[r] - Dl[j]) * p.scale;
           if constexpr (SOFTCAP) ds *= (1.0f - tv * tv);
           s[r] = pr;

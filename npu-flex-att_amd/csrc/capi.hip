@@ -34,6 +34,7 @@ int check_problem(const flexatt_problem* p) {
   if (p->batch <= 0 || p->heads_q <= 0 || p->heads_kv <= 0 || p->seqlen_q <= 0 || p->seqlen_kv <= 0)
     return FLEXATT_EINVAL;
   if (p->heads_q % p->heads_kv != 0) return FLEXATT_ESHAPE;
+  if (p->doc_bounds && p->seqlen_q != p->seqlen_kv) return FLEXATT_ESHAPE;
   if (head_index(p->head_dim) < 0) return FLEXATT_EHEADDIM;
   if (p->causal != 0 && p->causal != 1) return FLEXATT_EINVAL;
   if (p->sliding_window < 0) return FLEXATT_EINVAL;
@@ -70,6 +71,7 @@ Shape make_shape(const flexatt_problem* p) {
   s.cap = p->soft_cap;
   s.inv_cap = p->soft_cap > 0.f ? 1.0f / p->soft_cap : 0.f;
   s.alibi = p->alibi_slopes;
+  s.doc = p->doc_bounds;
   return s;
 }
 
@@ -97,7 +99,7 @@ const BwdLauncher kDkdv[3][4] = {
 constexpr int kDecWaves = 4;   // waves per workgroup
 constexpr int kDecTile = 32;   // KV rows per tile
 bool decode_applies(const flexatt_problem* p) {
-  return (p->dtype == FLEXATT_F16 || p->dtype == FLEXATT_BF16) && p->head_dim <= 128 &&
+  return (p->dtype == FLEXATT_F16 || p->dtype == FLEXATT_BF16) && p->head_dim <= 128 && !p->doc_bounds &&
          (int64_t)(p->heads_q / p->heads_kv) * p->seqlen_q <= 32;
 }
 struct DecodePlan {
@@ -128,6 +130,19 @@ const DecodeLauncher kDecode[3][3] = {
     {fwd_decode_f16_d32, fwd_decode_f16_d64, fwd_decode_f16_d128},
     {fwd_decode_bf16_d32, fwd_decode_bf16_d64, fwd_decode_bf16_d128},
 };
+
+// Document masks run on the general backward kernels (the D = 128 tile
+// streams have no document bounds).
+BwdLauncher pick_dq(const flexatt_problem* p) {
+  if (p->doc_bounds && p->head_dim == 128 && p->dtype != FLEXATT_F32)
+    return p->dtype == FLEXATT_BF16 ? bwd_dq_mfma_bf16_d128 : bwd_dq_mfma_f16_d128;
+  return kDq[p->dtype][head_index(p->head_dim)];
+}
+BwdLauncher pick_dkdv(const flexatt_problem* p) {
+  if (p->doc_bounds && p->head_dim == 128 && p->dtype != FLEXATT_F32)
+    return p->dtype == FLEXATT_BF16 ? bwd_dkdv_mfma_bf16_d128 : bwd_dkdv_mfma_f16_d128;
+  return kDkdv[p->dtype][head_index(p->head_dim)];
+}
 
 #define FLEXATT_TRY(x)             \
   do {                             \
@@ -252,7 +267,7 @@ int flexatt_bwd_dq(const flexatt_problem* p, const flexatt_tensor* q, const flex
   FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
   FLEXATT_TRY(check_tensor(dq, p->dtype));
   a.dq = mview(dq);
-  return (int)kDq[p->dtype][head_index(p->head_dim)](a, (hipStream_t)stream);
+  return (int)pick_dq(p)(a, (hipStream_t)stream);
 }
 
 int flexatt_bwd_dkdv(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
@@ -265,7 +280,7 @@ int flexatt_bwd_dkdv(const flexatt_problem* p, const flexatt_tensor* q, const fl
   FLEXATT_TRY(check_tensor(dv, p->dtype));
   a.dk = mview(dk);
   a.dv = mview(dv);
-  return (int)kDkdv[p->dtype][head_index(p->head_dim)](a, (hipStream_t)stream);
+  return (int)pick_dkdv(p)(a, (hipStream_t)stream);
 }
 
 int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
@@ -283,8 +298,8 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
   a.dk = mview(dk);
   a.dv = mview(dv);
   const int hi = head_index(p->head_dim);
-  FLEXATT_TRY((int)kDq[p->dtype][hi](a, (hipStream_t)stream));
-  return (int)kDkdv[p->dtype][hi](a, (hipStream_t)stream);
+  FLEXATT_TRY((int)pick_dq(p)(a, (hipStream_t)stream));
+  return (int)pick_dkdv(p)(a, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -57,6 +57,7 @@ struct Shape {
   float cap;          // 0 = off
   float inv_cap;
   const float* alibi;  // [Hq] or nullptr
+  const int* doc;      // [B][S][2] document bounds (Sq == Skv = S) or nullptr
 };
 
 // --- element traits ----------------------------------------------------------
@@ -292,6 +293,21 @@ __device__ __forceinline__ float score_log2(float s, const Shape& p, float slope
   }
   if constexpr (ALIBI) y += slope_log2 * (float)(i - j);
   return y;
+}
+
+// Document bounds [lo, hi) of position s of batch b: the other positions of
+// its document; [0, INT_MAX) when document masking is off.  Bounds are
+// non-decreasing in s, so those of a range's first and last positions bound
+// the whole range.
+__device__ __forceinline__ void doc_bounds(const Shape& p, int b, int s, int& lo, int& hi) {
+  if (p.doc) {
+    const int* d = p.doc + ((int64_t)b * p.Skv + s) * 2;
+    lo = d[0];
+    hi = d[1];
+  } else {
+    lo = 0;
+    hi = 0x7fffffff;
+  }
 }
 
 // allowed(i, j) for the masks of the path (j < Skv is the KV tail).

@@ -113,6 +113,16 @@ void fwd_mfma_kernel(FwdArgs a) {
   int kv_lo = 0, kv_hi = p.Skv;
   if (p.causal) kv_hi = min(kv_hi, m0 + bmh);
   if (p.window > 0) kv_lo = max(0, m0 - p.window);
+  // document masks: this lane's bounds and the KV range of the workgroup's rows
+  int dlo, dhi;
+  doc_bounds(p, b, min(my_m, p.Sq - 1), dlo, dhi);
+  if (p.doc) {
+    int l0, h0, l1, h1;
+    doc_bounds(p, b, min(m0, p.Sq - 1), l0, h0);
+    doc_bounds(p, b, min(m0 + bmh, p.Sq) - 1, l1, h1);
+    kv_lo = max(kv_lo, l0);
+    kv_hi = min(kv_hi, h1);
+  }
   const int t_lo = kv_lo / C::BN;
   const int t_hi = (kv_hi + C::BN - 1) / C::BN;
 
@@ -202,7 +212,7 @@ void fwd_mfma_kernel(FwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (!allowed(p, my_m, j)) s[bb][r] = kNegInf;
+          if (!allowed(p, my_m, j) || j < dlo || j >= dhi) s[bb][r] = kNegInf;
         }
     }
 
@@ -331,6 +341,17 @@ void fwd_mfma_kernel(FwdArgs a) {
     if (p.causal) tm_hi = min(tm_hi, (mw + 1) / C::BN);  // n0 + BN - 1 <= mw
     int tm_lo = 0;
     if (p.window > 0) tm_lo = max(0, (mw + 31 - p.window + C::BN - 1) / C::BN);  // mw + 31 - n0 <= window
+    if (p.doc) {  // full tiles lie inside the one document of all the wave's rows
+      int l0, h0, l1, h1;
+      doc_bounds(p, b, min(mw, p.Sq - 1), l0, h0);
+      doc_bounds(p, b, min(mw + 31, p.Sq - 1), l1, h1);
+      if (l0 == l1) {
+        tm_lo = max(tm_lo, (l0 + C::BN - 1) / C::BN);
+        tm_hi = min(tm_hi, h0 / C::BN);
+      } else {
+        tm_hi = tm_lo;
+      }
+    }
     tm_hi = __builtin_amdgcn_readfirstlane(tm_hi);
     tm_lo = __builtin_amdgcn_readfirstlane(tm_lo);
     auto softmax = [&](int n0) {
@@ -351,7 +372,7 @@ void fwd_mfma_kernel(FwdArgs a) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (!allowed(p, my_m, j)) s[bb][r] = kNegInf;
+            if (!allowed(p, my_m, j) || j < dlo || j >= dhi) s[bb][r] = kNegInf;
           }
           pin(s[bb]);  // finished inside the branch (no selects after it)
         }
@@ -494,7 +515,7 @@ void fwd_mfma_kernel(FwdArgs a) {
       // Per element masking only on tiles that cut the causal diagonal, the
       // window edge or the KV tail for some row of this wave.
       const bool need_mask = (n0 + C::BN > p.Skv) || (p.causal && n0 + C::BN - 1 > mw) ||
-                             (p.window > 0 && mw + 31 - n0 > p.window);
+                             (p.window > 0 && mw + 31 - n0 > p.window) || p.doc;
       tile_body(sK, sV, n0, need_mask);
       st = st == 2 ? 0 : st + 1;
     }

@@ -68,6 +68,15 @@ __global__ __launch_bounds__(256) void fwd_simt_kernel(FwdArgs a) {
   int kv_lo = 0, kv_hi = p.Skv;
   if (p.causal) kv_hi = min(kv_hi, m0 + kRows);
   if (p.window > 0) kv_lo = max(0, m0 - p.window);
+  int dlo, dhi;
+  doc_bounds(p, b, rq, dlo, dhi);
+  if (p.doc) {  // KV range of the block's documents
+    int l0, h0, l1, h1;
+    doc_bounds(p, b, min(m0, p.Sq - 1), l0, h0);
+    doc_bounds(p, b, min(m0 + kRows, p.Sq) - 1, l1, h1);
+    kv_lo = max(kv_lo, l0);
+    kv_hi = min(kv_hi, h1);
+  }
   float m_run = kNegInf, l_run = 0.f;
   for (int n0 = (kv_lo / kTile) * kTile; n0 < kv_hi; n0 += kTile) {
     __syncthreads();
@@ -89,7 +98,7 @@ __global__ __launch_bounds__(256) void fwd_simt_kernel(FwdArgs a) {
       const int j = n0 + jj;
       float t;
       float x = score(part, p, slope, my_m, j, t);
-      if (!allowed(p, my_m, j)) x = kNegInf;
+      if (!allowed(p, my_m, j) || j < dlo || j >= dhi) x = kNegInf;
       sc[jj] = x;
       mx = fmaxf(mx, x);
     }
@@ -150,6 +159,15 @@ __global__ __launch_bounds__(256) void bwd_dq_simt_kernel(BwdArgs a) {
   int kv_lo = 0, kv_hi = p.Skv;
   if (p.causal) kv_hi = min(kv_hi, m0 + kRows);
   if (p.window > 0) kv_lo = max(0, m0 - p.window);
+  int dlo, dhi;
+  doc_bounds(p, b, rq, dlo, dhi);
+  if (p.doc) {  // KV range of the block's documents
+    int l0, h0, l1, h1;
+    doc_bounds(p, b, min(m0, p.Sq - 1), l0, h0);
+    doc_bounds(p, b, min(m0 + kRows, p.Sq) - 1, l1, h1);
+    kv_lo = max(kv_lo, l0);
+    kv_hi = min(kv_hi, h1);
+  }
   for (int n0 = (kv_lo / kTile) * kTile; n0 < kv_hi; n0 += kTile) {
     __syncthreads();
     for (int idx = tid; idx < kTile * D; idx += 256) {
@@ -172,7 +190,7 @@ __global__ __launch_bounds__(256) void bwd_dq_simt_kernel(BwdArgs a) {
       const int j = n0 + jj;
       float t = 0.f;
       const float x = score(s, p, slope, my_m, j, t);
-      const float pj = allowed(p, my_m, j) ? expf(x - lse) : 0.f;
+      const float pj = (allowed(p, my_m, j) && j >= dlo && j < dhi) ? expf(x - lse) : 0.f;
       float ds = pj * (dpv - dl) * p.scale;
       if (p.cap > 0.f) ds *= (1.0f - t * t);
 #pragma unroll
@@ -210,6 +228,15 @@ __global__ __launch_bounds__(256) void bwd_dkdv_simt_kernel(BwdArgs a) {
   }
   int q_lo = p.causal ? n0 : 0, q_hi = p.Sq;
   if (p.window > 0) q_hi = min(q_hi, n0 + kRows + p.window);
+  int dlo, dhi;  // document masks are symmetric: the query range of this KV row
+  doc_bounds(p, b, rn, dlo, dhi);
+  if (p.doc) {
+    int l0, h0, l1, h1;
+    doc_bounds(p, b, min(n0, p.Skv - 1), l0, h0);
+    doc_bounds(p, b, min(n0 + kRows, p.Skv) - 1, l1, h1);
+    q_lo = max(q_lo, l0);
+    q_hi = min(q_hi, h1);
+  }
   for (int g = 0; g < p.G; ++g) {
     const int hq = hk * p.G + g;
     const float slope = p.alibi ? p.alibi[hq] : 0.f;
@@ -248,7 +275,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_simt_kernel(BwdArgs a) {
         const int m = m0 + ii;
         float t = 0.f;
         const float x = score(s, p, slope, m, my_n, t);
-        const float pj = (m < p.Sq && allowed(p, m, my_n)) ? expf(x - sL[ii]) : 0.f;
+        const float pj = (m < p.Sq && allowed(p, m, my_n) && m >= dlo && m < dhi) ? expf(x - sL[ii]) : 0.f;
         float ds = pj * (dpv - sDl[ii]) * p.scale;
         if (p.cap > 0.f) ds *= (1.0f - t * t);
 #pragma unroll

@@ -26,7 +26,7 @@ EXPORTS = (
     "flexatt_status_string",
     "flexatt_abi_version",
 )
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class Tensor(ctypes.Structure):
@@ -57,6 +57,7 @@ class Problem(ctypes.Structure):
         ("sliding_window", ctypes.c_int32),
         ("soft_cap", ctypes.c_float),
         ("alibi_slopes", ctypes.c_void_p),
+        ("doc_bounds", ctypes.c_void_p),
     ]
 
 

@@ -74,7 +74,7 @@ def _check_device_dtype(name_tensors, dtype):
             raise RuntimeError(f"{name} has dtype {t.dtype}, expected {dtype}")
 
 
-def _problem(query, key, scale, causal, sliding_window, soft_cap, alibi):
+def _problem(query, key, scale, causal, sliding_window, soft_cap, alibi, doc=None):
     B, Hq, Sq, D = query.shape
     Hkv, Sk = key.shape[1], key.shape[2]
     if query.dtype not in _DTYPES:
@@ -91,6 +91,7 @@ def _problem(query, key, scale, causal, sliding_window, soft_cap, alibi):
     p.sliding_window = int(sliding_window) if sliding_window and sliding_window > 0 else 0
     p.soft_cap = float(soft_cap) if soft_cap and soft_cap > 0.0 else 0.0
     p.alibi_slopes = alibi.data_ptr() if alibi is not None else None
+    p.doc_bounds = doc.data_ptr() if doc is not None else None
     return p
 
 
@@ -101,6 +102,29 @@ def _alibi(alibi_slope, hq, device):
     if s.numel() != hq:
         raise RuntimeError(f"alibi_slope must have Hq={hq} entries, got {s.numel()}")
     return s
+
+
+def _doc_bounds(document_ids, B, Sq, Sk, device):
+    """Document masks: ``document_ids`` [B, S] (S = Sq = Skv) -> int32
+    [B, S, 2] holding, per position, the range [lo, hi) of its document, a
+    maximal run of equal ids.  Positions of different documents do not attend
+    to each other."""
+    if document_ids is None:
+        return None
+    ids = torch.as_tensor(document_ids, device=device)
+    if ids.dim() != 2 or ids.shape[0] != B or ids.shape[1] != Sk or Sq != Sk:
+        raise RuntimeError(f"document_ids must be [B, S] = [{B}, {Sk}] with Sq == Skv (got {tuple(ids.shape)}, Sq={Sq})")
+    if ids.dtype.is_floating_point or ids.dtype == torch.bool:
+        raise RuntimeError("document_ids must be an integer tensor")
+    S = Sk
+    pos = torch.arange(S, device=device, dtype=torch.int32).expand(B, S)
+    start = torch.ones(B, S, dtype=torch.bool, device=device)
+    start[:, 1:] = ids[:, 1:] != ids[:, :-1]
+    end = torch.ones(B, S, dtype=torch.bool, device=device)
+    end[:, :-1] = start[:, 1:]
+    lo = torch.where(start, pos, torch.zeros_like(pos)).cummax(dim=1).values
+    hi = torch.where(end, pos + 1, torch.full_like(pos, S)).flip(1).cummin(dim=1).values.flip(1)
+    return torch.stack((lo, hi), dim=-1).to(torch.int32).contiguous()
 
 
 def _stream(device):
@@ -118,13 +142,16 @@ def npu_flash_attention_forward(
     block_n=64,
     return_lse=False,
     soft_cap=0.0,
+    document_ids=None,
 ):
     """Attention forward; returns ``O`` or ``(O, LSE)``.
 
     ``O`` has ``query``'s dtype and layout (``empty_like``), ``LSE`` is fp32
     ``[B, Hq, Sq]`` in natural log.  Follows npu_flash_attention.py:606-656:
     the same shape assertions (:620-622) and default scale ``1/sqrt(D)``
-    (:625-626).
+    (:625-626).  ``document_ids`` ([B, S] integers, Sq == Skv; no counterpart
+    in the reference) adds a document mask: positions of different runs of
+    equal ids do not attend to each other.
     """
     B, Hq, Sq, D = query.shape
     Bk, Hkv, Sk, Dk = key.shape
@@ -143,14 +170,15 @@ def npu_flash_attention_forward(
     if not _kernel_ready(O):
         O = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     LSE = torch.empty(B, Hq, Sq, device=query.device, dtype=torch.float32)
+    doc = _doc_bounds(document_ids, B, Sq, Sk, query.device)
     _forward_into(query, key, value, O, LSE, causal=causal, sliding_window=sliding_window,
-                  alibi=alibi_slope, scale=scale, soft_cap=soft_cap)
+                  alibi=alibi_slope, scale=scale, soft_cap=soft_cap, doc=doc)
     if return_lse:
         return O, LSE
     return O
 
 
-def _forward_into(query, key, value, O, LSE, *, causal, sliding_window, alibi, scale, soft_cap):
+def _forward_into(query, key, value, O, LSE, *, causal, sliding_window, alibi, scale, soft_cap, doc=None):
     """Run the forward kernels into the caller's ``O`` (kernel-ready layout)
     and contiguous fp32 ``LSE``; shapes are already validated."""
     if O.numel() == 0 or key.shape[2] == 0:
@@ -160,7 +188,7 @@ def _forward_into(query, key, value, O, LSE, *, causal, sliding_window, alibi, s
     lib = _lib.load()
     q, k, v = _prepare(query), _prepare(key), _prepare(value)
     slopes = _alibi(alibi, query.shape[1], query.device)
-    p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes)
+    p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes, doc)
     # Few query rows per KV head (decoding): the split-KV kernels, with their
     # partial results in a workspace from torch's caching allocator.
     ws_bytes = lib.flexatt_fwd_decode_workspace(p) if decode_enabled else 0
@@ -186,6 +214,7 @@ def npu_flash_attention_backward(
     block_m=16,
     block_n=32,
     soft_cap=0.0,
+    document_ids=None,
 ):
     """Attention backward; returns ``(dQ, dK, dV)``.
 
@@ -215,13 +244,14 @@ def npu_flash_attention_backward(
         DQ = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     DK = torch.empty(B, Hkv, Sk, D, device=key.device, dtype=key.dtype)
     DV = torch.empty(B, Hkv, Sk, D, device=value.device, dtype=value.dtype)
+    doc = _doc_bounds(document_ids, B, Sq, Sk, query.device)
     _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, causal=causal,
-                   sliding_window=sliding_window, alibi=alibi_slope, scale=scale, soft_cap=soft_cap)
+                   sliding_window=sliding_window, alibi=alibi_slope, scale=scale, soft_cap=soft_cap, doc=doc)
     return DQ, DK, DV
 
 
 def _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, *, causal, sliding_window,
-                   alibi, scale, soft_cap):
+                   alibi, scale, soft_cap, doc=None):
     """Run Delta, dQ and dK/dV into the caller's ``DQ`` (kernel-ready layout)
     and contiguous ``DK`` / ``DV``; shapes are already validated."""
     if DQ.numel() == 0 or DK.numel() == 0:
@@ -236,7 +266,7 @@ def _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, *, causal,
     o, do = _prepare(out), _prepare(grad_out)
     lse = lse.to(torch.float32).contiguous()
     slopes = _alibi(alibi, Hq, query.device)
-    p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes)
+    p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes, doc)
     with torch.cuda.device(query.device):
         st = lib.flexatt_bwd(p, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v), _lib.tensor(o),
                              _lib.tensor(do), lse.data_ptr(), delta.data_ptr(), _lib.tensor(DQ),
@@ -254,7 +284,7 @@ class NPUFlexAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, query, key, value, causal=False, sliding_window=0,
-                alibi_slope=None, scale=None, block_m=16, block_n=64, soft_cap=0.0):
+                alibi_slope=None, scale=None, block_m=16, block_n=64, soft_cap=0.0, document_ids=None):
         ctx.causal = causal
         ctx.sliding_window = sliding_window
         ctx.alibi_slope = alibi_slope
@@ -262,13 +292,14 @@ class NPUFlexAttention(torch.autograd.Function):
         ctx.block_m = block_m
         ctx.block_n = block_n
         ctx.soft_cap = soft_cap
+        ctx.document_ids = document_ids
         with torch.no_grad():
             out, lse = npu_flash_attention_forward(
                 query, key, value,
                 causal=causal, sliding_window=sliding_window,
                 alibi_slope=alibi_slope, scale=scale,
                 block_m=block_m, block_n=block_n, return_lse=True,
-                soft_cap=soft_cap,
+                soft_cap=soft_cap, document_ids=document_ids,
             )
         ctx.save_for_backward(query, key, value, lse, out)
         return out
@@ -281,9 +312,9 @@ class NPUFlexAttention(torch.autograd.Function):
             causal=ctx.causal, sliding_window=ctx.sliding_window,
             alibi_slope=ctx.alibi_slope, scale=ctx.scale,
             block_m=ctx.block_m, block_n=ctx.block_n,
-            soft_cap=ctx.soft_cap,
+            soft_cap=ctx.soft_cap, document_ids=ctx.document_ids,
         )
-        return DQ, DK, DV, None, None, None, None, None, None, None
+        return DQ, DK, DV, None, None, None, None, None, None, None, None
 
 
 def npu_flex_attention(
@@ -292,11 +323,13 @@ def npu_flex_attention(
     alibi_slope=None, scale=None,
     block_m=16, block_n=64,
     soft_cap=0.0,
+    document_ids=None,
 ):
-    """Autograd entry point (npu_flash_attention.py:784-794)."""
+    """Autograd entry point (npu_flash_attention.py:784-794); ``document_ids``
+    as in :func:`npu_flash_attention_forward`."""
     return NPUFlexAttention.apply(
         query, key, value, causal, sliding_window,
-        alibi_slope, scale, block_m, block_n, soft_cap,
+        alibi_slope, scale, block_m, block_n, soft_cap, document_ids,
     )
 
 
@@ -322,6 +355,7 @@ class AttentionConfig:
     soft_cap: float = 0.0
     block_m: int = 16
     block_n: int = 64
+    document_ids: Optional[torch.Tensor] = None  # no counterpart in the reference
 
     def __post_init__(self):
         if self.sliding_window < 0:
@@ -348,4 +382,5 @@ def flex_attention(query, key, value, config: Optional[AttentionConfig] = None, 
         block_m=config.block_m,
         block_n=config.block_n,
         soft_cap=config.soft_cap,
+        document_ids=config.document_ids,
     )

@@ -20,6 +20,8 @@ every primitive the kernels implement:
 * softmax with natural-log LSE, fully-masked rows give ``O=0, LSE=-inf``
   (npu_flash_attention.py:152-166);
 * GQA: query head ``h`` reads KV head ``h // G`` (npu_flash_attention.py:42);
+* document masks (no counterpart in the reference, see :func:`document_mask`):
+  pairs in different runs of ``document_ids`` are masked;
 * backward: ``Delta = rowsum(O*dO)`` (npu_flash_attention.py:681-685),
   ``dS = P*(dP-Delta)*scale*(1-tanh^2)`` (npu_flash_attention.py:386-399,
   :502-516), dK/dV summed over the G query heads of a group
@@ -42,6 +44,7 @@ import torch
 
 __all__ = [
     "allowed_mask",
+    "document_mask",
     "scores",
     "forward",
     "delta",
@@ -68,6 +71,29 @@ def allowed_mask(sq: int, skv: int, causal: bool, sliding_window: int) -> torch.
         ok &= j <= i
     if sliding_window > 0:
         ok &= (i - j) <= sliding_window
+    return ok
+
+
+def document_mask(document_ids: torch.Tensor) -> torch.Tensor:
+    """Boolean [B, 1, S, S] mask of pairs in the same document.
+
+    Document masking has no counterpart in the reference (it is one of the
+    future candidates it lists, README.md:219; DESIGN.md:374, :382).  Here a
+    document is a maximal run of equal values along a row of
+    ``document_ids`` [B, S]: positions i and j attend to each other only
+    inside one run (on top of the other primitives).
+    """
+    ids = document_ids.detach().to("cpu").long()
+    change = torch.zeros_like(ids)
+    change[:, 1:] = (ids[:, 1:] != ids[:, :-1]).long()
+    run = torch.cumsum(change, dim=1)
+    return (run.unsqueeze(-1) == run.unsqueeze(-2)).unsqueeze(1)
+
+
+def _mask(sq, skv, causal, sliding_window, document_ids):
+    ok = allowed_mask(sq, skv, causal, sliding_window)
+    if document_ids is not None:
+        ok = ok & document_mask(document_ids)
     return ok
 
 
@@ -138,6 +164,7 @@ def forward(
     scale: Optional[float] = None,
     soft_cap: float = 0.0,
     dtype: torch.dtype = torch.float64,
+    document_ids: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Eager attention forward: returns (O [B,Hq,Sq,D], LSE [B,Hq,Sq]).
 
@@ -147,7 +174,7 @@ def forward(
     """
     qf, kf, vf, scale, _ = _prep(q, k, v, scale, dtype)
     x, _ = scores(qf, kf, scale, soft_cap, alibi_slope)
-    ok = allowed_mask(x.shape[-2], x.shape[-1], causal, sliding_window)
+    ok = _mask(x.shape[-2], x.shape[-1], causal, sliding_window, document_ids)
     p, lse = _softmax_masked(x, ok)
     return torch.matmul(p, vf), lse
 
@@ -169,6 +196,7 @@ def backward(
     soft_cap: float = 0.0,
     dtype: torch.dtype = torch.float64,
     o: Optional[torch.Tensor] = None,
+    document_ids: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Closed-form attention backward: (dQ, dK, dV), dK/dV in [B,Hkv,Skv,D].
 
@@ -185,7 +213,7 @@ def backward(
     qf, kf, vf, scale, g = _prep(q, k, v, scale, dtype)
     dof = do.detach().to("cpu", dtype)
     x, t = scores(qf, kf, scale, soft_cap, alibi_slope)
-    ok = allowed_mask(sq, x.shape[-1], causal, sliding_window)
+    ok = _mask(sq, x.shape[-1], causal, sliding_window, document_ids)
     p, _ = _softmax_masked(x, ok)
     of = torch.matmul(p, vf) if o is None else o.detach().to("cpu", dtype)
     dl = (of * dof).sum(-1, keepdim=True)
@@ -204,7 +232,7 @@ def backward(
 
 
 def backward_autograd(q, k, v, do, causal=False, sliding_window=0, alibi_slope=None,
-                      scale=None, soft_cap=0.0, dtype=torch.float64):
+                      scale=None, soft_cap=0.0, dtype=torch.float64, document_ids=None):
     """(dQ, dK, dV) by autograd through :func:`forward` — the form of the
     reference's oracle ``ref_sdpa_backward`` (test/test_comprehensive.py:54-60);
     GQA K/V gradients come out summed over the group because the expansion is
@@ -216,7 +244,7 @@ def backward_autograd(q, k, v, do, causal=False, sliding_window=0, alibi_slope=N
     g = hq // hkv
     sc = (1.0 / math.sqrt(q.shape[-1])) if scale is None else float(scale)
     x, _ = scores(qr, _expand_kv(kr, g), sc, soft_cap, alibi_slope)
-    ok = allowed_mask(x.shape[-2], x.shape[-1], causal, sliding_window)
+    ok = _mask(x.shape[-2], x.shape[-1], causal, sliding_window, document_ids)
     p, _ = _softmax_masked(x, ok)
     o = torch.matmul(p, _expand_kv(vr, g))
     o.backward(do.detach().to("cpu", dtype))

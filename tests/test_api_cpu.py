@@ -70,3 +70,32 @@ def test_kernel_ready_layout_rules():
     assert not nfa._kernel_ready(t.transpose(2, 3))           # innermost stride != 1
     assert nfa._kernel_ready(t[:, :1].expand(2, 3, 8, 64))     # stride-0 heads are fine
     assert not nfa._kernel_ready(torch.randn(1, 1, 8, 65)[..., :64])  # rows not 16-byte aligned
+
+
+# ------------------------------------------------------------ document masks --
+def test_document_bounds_match_oracle_mask():
+    """The host-side bounds ([lo, hi) per position) describe exactly the
+    oracle's document mask (runs of equal ids)."""
+    from oracle import attention_oracle as orc
+
+    ids = torch.tensor([[0, 0, 0, 1, 1, 2, 2, 2, 2, 3, 0, 0, 0], [5] * 7 + [6] * 6, [9] * 13])
+    bounds = nfa._doc_bounds(ids, 3, 13, 13, "cpu")
+    assert bounds.dtype == torch.int32 and bounds.shape == (3, 13, 2) and bounds.is_contiguous()
+    j = torch.arange(13)
+    mask = (j.view(1, 1, 13) >= bounds[..., :1]) & (j.view(1, 1, 13) < bounds[..., 1:])
+    assert torch.equal(mask.unsqueeze(1), orc.document_mask(ids))
+
+
+def test_document_ids_rejected_when_malformed():
+    ids = torch.zeros(1, 16, dtype=torch.int64)
+    with pytest.raises(RuntimeError):
+        nfa._doc_bounds(ids, 1, 8, 16, "cpu")           # Sq != Skv
+    with pytest.raises(RuntimeError):
+        nfa._doc_bounds(ids, 2, 16, 16, "cpu")          # batch mismatch
+    with pytest.raises(RuntimeError):
+        nfa._doc_bounds(ids.float(), 1, 16, 16, "cpu")  # not integers
+
+
+def test_attention_config_carries_document_ids():
+    cfg = nfa.AttentionConfig(causal=True, document_ids=torch.zeros(1, 4, dtype=torch.int32))
+    assert cfg.document_ids is not None and cfg.causal

@@ -31,22 +31,23 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_status_strings():
     lib = L.load()
     assert lib.flexatt_abi_version() == L.ABI_VERSION
-    assert b"#define FLEXATT_ABI_VERSION 2" in open(HEADER, "rb").read()
+    assert b"#define FLEXATT_ABI_VERSION 3" in open(HEADER, "rb").read()
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.flexatt_status_string(code)
     assert b"head_dim" in lib.flexatt_status_string(-3)
 
 
 def test_struct_layout_matches_header():
-    # flexatt_tensor: pointer + 4 x int64; flexatt_problem: 7 int32, float, 2 int32, float, pointer
+    # flexatt_tensor: pointer + 4 x int64; flexatt_problem: 7 int32, float, 2 int32, float, 2 pointers
     assert ctypes.sizeof(L.Tensor) == 40
-    assert L.Problem.alibi_slopes.offset == 48 and ctypes.sizeof(L.Problem) == 56
+    assert L.Problem.alibi_slopes.offset == 48 and L.Problem.doc_bounds.offset == 56
+    assert ctypes.sizeof(L.Problem) == 64
 
 
 def problem(**kw):
     p = L.Problem()
     vals = dict(dtype=L.BF16, batch=1, heads_q=4, heads_kv=2, seqlen_q=64, seqlen_kv=64, head_dim=64,
-                scale=0.125, causal=1, sliding_window=0, soft_cap=0.0, alibi_slopes=None)
+                scale=0.125, causal=1, sliding_window=0, soft_cap=0.0, alibi_slopes=None, doc_bounds=None)
     vals.update(kw)
     for k, v in vals.items():
         setattr(p, k, v)

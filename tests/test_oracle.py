@@ -296,3 +296,61 @@ def test_planted_mistakes_are_caught(monkeypatch):
     bo, _ = brute_forward(q, k, v, True, 0, None, None, 0.0)
     wrong, _ = gqa_modulo(q, k, v, True, 0, None, None, 0.0)
     assert not torch.allclose(wrong, bo, atol=1e-9)
+
+
+# ------------------------------------------------------------- document masks --
+DOC_IDS = torch.tensor([[0, 0, 0, 1, 1, 2, 2, 2, 2, 3, 0, 0, 0],
+                        [5, 5, 5, 5, 5, 5, 5, 6, 6, 6, 6, 6, 6]])
+
+
+def _runs(ids_row):
+    """[(start, end)] of the maximal runs of equal values."""
+    out, s = [], 0
+    for t in range(1, len(ids_row) + 1):
+        if t == len(ids_row) or ids_row[t] != ids_row[t - 1]:
+            out.append((s, t))
+            s = t
+    return out
+
+
+@pytest.mark.parametrize("causal,window,alibi,cap", [(False, 0, False, 0.0), (True, 0, False, 0.0),
+                                                      (True, 2, True, 1.3), (False, 3, False, 0.9)])
+def test_document_mask_equals_independent_segments(causal, window, alibi, cap):
+    """Attention with document masks = attention run on each document alone
+    (the primitives depend only on i - j, so slicing preserves them); rows and
+    gradients of one document do not see any other."""
+    b, hq, hkv, s, d = 2, 4, 2, DOC_IDS.shape[1], 8
+    q, k, v, do = rnd(b, hq, s, d, seed=60), rnd(b, hkv, s, d, seed=61), rnd(b, hkv, s, d, seed=62), rnd(b, hq, s, d, seed=63)
+    slopes = torch.tensor([0.3, -0.2, 0.5, 0.1]) if alibi else None
+    o, lse = orc.forward(q, k, v, causal, window, slopes, 0.6, cap, document_ids=DOC_IDS)
+    dq, dk, dv = orc.backward(q, k, v, do, causal, window, slopes, 0.6, cap, document_ids=DOC_IDS)
+    for bi in range(b):
+        for a, e in _runs(DOC_IDS[bi].tolist()):
+            sl = (slice(bi, bi + 1), slice(None), slice(a, e))
+            os_, ls_ = orc.forward(q[sl], k[sl], v[sl], causal, window, slopes, 0.6, cap)
+            dqs, dks, dvs = orc.backward(q[sl], k[sl], v[sl], do[sl], causal, window, slopes, 0.6, cap)
+            assert torch.allclose(o[sl], os_, atol=1e-12)
+            assert torch.equal(torch.isinf(lse[sl]), torch.isinf(ls_))
+            fin = torch.isfinite(ls_)
+            assert torch.allclose(lse[sl][fin], ls_[fin], atol=1e-12)
+            assert torch.allclose(dq[sl], dqs, atol=1e-12)
+            assert torch.allclose(dk[sl], dks, atol=1e-12)
+            assert torch.allclose(dv[sl], dvs, atol=1e-12)
+
+
+def test_document_runs_not_values():
+    """A repeated id after another one starts a new document (runs, not equal
+    values): positions 0-2 and 10-12 of row 0 above do not attend to each
+    other."""
+    m = orc.document_mask(DOC_IDS)
+    assert m.shape == (2, 1, 13, 13)
+    assert not bool(m[0, 0, 0, 11]) and not bool(m[0, 0, 12, 1])
+    assert bool(m[0, 0, 11, 12]) and bool(m[1, 0, 0, 6]) and not bool(m[1, 0, 6, 7])
+
+
+def test_document_backward_closed_form_matches_autograd():
+    q, k, v, do = rnd(2, 4, 13, 8, seed=64), rnd(2, 2, 13, 8, seed=65), rnd(2, 2, 13, 8, seed=66), rnd(2, 4, 13, 8, seed=67)
+    a = orc.backward(q, k, v, do, True, 0, None, 0.5, 0.0, document_ids=DOC_IDS)
+    b = orc.backward_autograd(q, k, v, do, True, 0, None, 0.5, 0.0, document_ids=DOC_IDS)
+    for x, y in zip(a, b):
+        assert torch.allclose(x, y, atol=1e-11)
