@@ -48,6 +48,9 @@ struct BwdCfg {
   static constexpr int BMQ = 64;
   static constexpr int CPTQ = BMQ * CPR / (NW * 64);
   static constexpr bool PREFETCH = D <= 128;
+  // D = 256: dV and dK in two passes over the query tiles (S recomputed), so
+  // that the K / V rows and both accumulator sets never share the registers
+  static constexpr bool SPLIT = D == 256;
 };
 
 // ---------------------------------------------------------------- dQ kernel --
@@ -248,21 +251,17 @@ __global__ __launch_bounds__(256) void bwd_dkdv_mfma_kernel(BwdArgs a) {
   const int nw = n0 + wave * 32;
   const int my_n = nw + l32;
 
-  V8 kf[C::KC], vf[C::KC];
-  {
-    const T* kp = (const T*)a.k.data + b * a.k.sb + hk * a.k.sh;
-    const T* vp = (const T*)a.v.data + b * a.v.sb + hk * a.v.sh;
-    const int r = min(my_n, p.Skv - 1);
-    const T* sk = kp + (int64_t)r * a.k.ss + 8 * h;
-    const T* sv = vp + (int64_t)r * a.v.ss + 8 * h;
+  // K / V rows of this lane as MFMA B operands (k = 8 consecutive d).
+  const int rkv = min(my_n, p.Skv - 1);
+  auto load_rows = [&](const View& t, V8 (&f)[C::KC]) {
+    const T* src = (const T*)t.data + b * t.sb + hk * t.sh + (int64_t)rkv * t.ss + 8 * h;
 #pragma unroll
     for (int kc = 0; kc < C::KC; ++kc) {
-      i32x4 x = ld_global16(sk + 16 * kc), y = ld_global16(sv + 16 * kc);
-      if (my_n >= p.Skv) { x = i32x4{0, 0, 0, 0}; y = i32x4{0, 0, 0, 0}; }
-      kf[kc] = as_v8<V8>(x);
-      vf[kc] = as_v8<V8>(y);
+      i32x4 x = ld_global16(src + 16 * kc);
+      if (my_n >= p.Skv) x = i32x4{0, 0, 0, 0};
+      f[kc] = as_v8<V8>(x);
     }
-  }
+  };
 
   int q_lo = p.causal ? n0 : 0;
   int q_hi = p.Sq;
@@ -331,94 +330,141 @@ __global__ __launch_bounds__(256) void bwd_dkdv_mfma_kernel(BwdArgs a) {
     }
   };
 
+  V8 kf[C::KC], vf[C::KC];
   f32x16 adk[C::DB], adv[C::DB];
-#pragma unroll
-  for (int db = 0; db < C::DB; ++db) {
-    adk[db] = f32x16{};
-    adv[db] = f32x16{};
-  }
 
-  if (C::PREFETCH && iters > 0) gload(0);
-  for (int it = 0; it < iters; ++it) {
-    if (it > 0) __syncthreads();
-    if (!C::PREFETCH) gload(it);
-    lstore();
-    __syncthreads();
-    if (C::PREFETCH && it + 1 < iters) gload(it + 1);
+  // One pass over the query tiles of the group, accumulating dV^T (DV) and/or
+  // dK^T (DK).  A dV-only pass needs neither dP nor the V rows.
+  auto run = [&](auto dv_c, auto dk_c) {
+    constexpr bool DV = decltype(dv_c)::value, DK = decltype(dk_c)::value;
+    if (C::PREFETCH && iters > 0) gload(0);
+    for (int it = 0; it < iters; ++it) {
+      if (it > 0) __syncthreads();
+      if (!C::PREFETCH) gload(it);
+      lstore();
+      __syncthreads();
+      if (C::PREFETCH && it + 1 < iters) gload(it + 1);
 
-    const int g = it / nq;
-    const int hq = hk * p.G + g;
-    const int mt = (qt_lo + it % nq) * C::BMQ;
-    const bool skip = (p.causal && mt + C::BMQ - 1 < nw) || (p.window > 0 && mt - (nw + 31) > p.window) ||
-                      mt >= whi || mt + C::BMQ <= wlo;
-    if (skip) continue;
-    const bool full = (!p.causal || mt >= nw + 31) && (p.window == 0 || mt + C::BMQ - 1 - nw <= p.window) &&
-                      !p.doc;
-    const float slope_log2 = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
-    const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+      const int g = it / nq;
+      const int hq = hk * p.G + g;
+      const int mt = (qt_lo + it % nq) * C::BMQ;
+      const bool skip = (p.causal && mt + C::BMQ - 1 < nw) || (p.window > 0 && mt - (nw + 31) > p.window) ||
+                        mt >= whi || mt + C::BMQ <= wlo;
+      if (skip) continue;
+      const bool full = (!p.causal || mt >= nw + 31) && (p.window == 0 || mt + C::BMQ - 1 - nw <= p.window) &&
+                        !p.doc;
+      const float slope_log2 = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
+      const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
 #pragma unroll
-    for (int mb = 0; mb < C::BMQ / 32; ++mb) {
-      f32x16 s = f32x16{}, dp = f32x16{};
-      const T* qr = sQ + (32 * mb + l32) * C::P + 8 * h;
-      const T* orr = sO + (32 * mb + l32) * C::P + 8 * h;
+      for (int mb = 0; mb < C::BMQ / 32; ++mb) {
+        __builtin_amdgcn_sched_barrier(0);
+        f32x16 s = f32x16{}, dp = f32x16{};
+        const T* qr = sQ + (32 * mb + l32) * C::P + 8 * h;
+        const T* orr = sO + (32 * mb + l32) * C::P + 8 * h;
+        // row reads kept RA k-steps ahead in a small ring (fenced, so that the
+        // compiler does not hoist all KC of them into registers at once)
+        constexpr int RA = 2;
+        i32x4 aq[RA + 1], ao[RA + 1];
 #pragma unroll
-      for (int kc = 0; kc < C::KC; ++kc) {
-        s = M::mma(as_v8<V8>(lds_read16(qr + 16 * kc)), kf[kc], s);
-        dp = M::mma(as_v8<V8>(lds_read16(orr + 16 * kc)), vf[kc], dp);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int mr = 32 * mb + 8 * i + 4 * h;
-        const f32x4 L = *(const f32x4*)&sL[mr];
-        const f32x4 Dl = *(const f32x4*)&sDl[mr];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = 4 * i + j;
-          const int m = mt + mr + j;
-          float tv = 0.f;
-          const float y = score_log2<SOFTCAP, ALIBI>(s[r], p, slope_log2, m, my_n, tv);
-          float pr = fast_exp2(y - L[j]);
-          if (!full && (!allowed(p, m, my_n) || m < dlo || m >= dhi)) pr = 0.f;
-          float ds = pr * (dp[r] - Dl[j]) * p.scale;
-          if constexpr (SOFTCAP) ds *= (1.0f - tv * tv);
-          s[r] = pr;
-          dp[r] = ds;
+        for (int kc = 0; kc < RA; ++kc) {
+          aq[kc] = lds_read16(qr + 16 * kc);
+          if constexpr (DK) ao[kc] = lds_read16(orr + 16 * kc);
         }
-      }
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const V8 pb = pack8<T>(s, 8 * c);
-        const V8 dsb = pack8<T>(dp, 8 * c);
-        const int row = 32 * mb + 16 * c + 4 * h + ((lane & 15) >> 2);
-        const T* orow = sO + row * C::P + tr_col;
-        const T* qrow = sQ + row * C::P + tr_col;
+        for (int kc = 0; kc < C::KC; ++kc) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (kc + RA < C::KC) {
+            aq[(kc + RA) % (RA + 1)] = lds_read16(qr + 16 * (kc + RA));
+            if constexpr (DK) ao[(kc + RA) % (RA + 1)] = lds_read16(orr + 16 * (kc + RA));
+          }
+          s = M::mma(as_v8<V8>(aq[kc % (RA + 1)]), kf[kc], s);
+          if constexpr (DK) dp = M::mma(as_v8<V8>(ao[kc % (RA + 1)]), vf[kc], dp);
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int db = 0; db < C::DB; ++db) {
-          const i16x4 olo = lds_read_tr4(orow + 32 * db);
-          const i16x4 ohi = lds_read_tr4(orow + 8 * C::P + 32 * db);
-          adv[db] = M::mma(cat_tr<V8>(olo, ohi), pb, adv[db]);
-          const i16x4 qlo = lds_read_tr4(qrow + 32 * db);
-          const i16x4 qhi = lds_read_tr4(qrow + 8 * C::P + 32 * db);
-          adk[db] = M::mma(cat_tr<V8>(qlo, qhi), dsb, adk[db]);
+        for (int i = 0; i < 4; ++i) {
+          const int mr = 32 * mb + 8 * i + 4 * h;
+          const f32x4 L = *(const f32x4*)&sL[mr];
+          const f32x4 Dl = *(const f32x4*)&sDl[mr];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * i + j;
+            const int m = mt + mr + j;
+            float tv = 0.f;
+            const float y = score_log2<SOFTCAP, ALIBI>(s[r], p, slope_log2, m, my_n, tv);
+            float pr = fast_exp2(y - L[j]);
+            if (!full && (!allowed(p, m, my_n) || m < dlo || m >= dhi)) pr = 0.f;
+            s[r] = pr;
+            if constexpr (DK) {
+              float ds = pr * (dp[r] - Dl[j]) * p.scale;
+              if constexpr (SOFTCAP) ds *= (1.0f - tv * tv);
+              dp[r] = ds;
+            }
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int row = 32 * mb + 16 * c + 4 * h + ((lane & 15) >> 2);
+          const T* orow = sO + row * C::P + tr_col;
+          const T* qrow = sQ + row * C::P + tr_col;
+          // transpose reads one MFMA ahead (fenced: a two-entry ring)
+          auto tr_mma = [&](const T* base, const V8 op, f32x16 (&acc)[C::DB]) {
+            i16x4 lo[2], hi[2];
+            lo[0] = lds_read_tr4(base);
+            hi[0] = lds_read_tr4(base + 8 * C::P);
+#pragma unroll
+            for (int db = 0; db < C::DB; ++db) {
+              __builtin_amdgcn_sched_barrier(0);
+              if (db + 1 < C::DB) {
+                lo[(db + 1) & 1] = lds_read_tr4(base + 32 * (db + 1));
+                hi[(db + 1) & 1] = lds_read_tr4(base + 8 * C::P + 32 * (db + 1));
+              }
+              acc[db] = M::mma(cat_tr<V8>(lo[db & 1], hi[db & 1]), op, acc[db]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          };
+          if constexpr (DV) tr_mma(orow, pack8<T>(s, 8 * c), adv);
+          if constexpr (DK) tr_mma(qrow, pack8<T>(dp, 8 * c), adk);
         }
       }
     }
-  }
+  };
+  auto store = [&](const MutView& t, const f32x16 (&acc)[C::DB], float sc) {
+    if (my_n < p.Skv) {
+      T* dst = (T*)t.data + b * t.sb + hk * t.sh + (int64_t)my_n * t.ss + 4 * h;
+#pragma unroll
+      for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          st_global8(dst + 32 * db + 8 * i, pack4<T>(acc[db][4 * i] * sc, acc[db][4 * i + 1] * sc,
+                                                    acc[db][4 * i + 2] * sc, acc[db][4 * i + 3] * sc));
+    }
+  };
 
-  if (my_n < p.Skv) {
-    T* kp = (T*)a.dk.data + b * a.dk.sb + hk * a.dk.sh + (int64_t)my_n * a.dk.ss + 4 * h;
-    T* vp = (T*)a.dv.data + b * a.dv.sb + hk * a.dv.sh + (int64_t)my_n * a.dv.ss + 4 * h;
+  load_rows(a.k, kf);
+  if constexpr (C::SPLIT) {
+    // dV, then dK: only one accumulator set is live at a time
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db) adv[db] = f32x16{};
+    run(std::true_type{}, std::false_type{});
+    store(a.dv, adv, 1.0f);
+    load_rows(a.v, vf);
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db) adk[db] = f32x16{};
+    __syncthreads();  // the first pass's last tile has been read
+    run(std::false_type{}, std::true_type{});
+    store(a.dk, adk, 1.0f);
+  } else {
+    load_rows(a.v, vf);
 #pragma unroll
     for (int db = 0; db < C::DB; ++db) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        st_global8(kp + 32 * db + 8 * i,
-                   pack4<T>(adk[db][4 * i], adk[db][4 * i + 1], adk[db][4 * i + 2], adk[db][4 * i + 3]));
-        st_global8(vp + 32 * db + 8 * i,
-                   pack4<T>(adv[db][4 * i], adv[db][4 * i + 1], adv[db][4 * i + 2], adv[db][4 * i + 3]));
-      }
+      adk[db] = f32x16{};
+      adv[db] = f32x16{};
     }
+    run(std::true_type{}, std::true_type{});
+    store(a.dv, adv, 1.0f);
+    store(a.dk, adk, 1.0f);
   }
 }
 
