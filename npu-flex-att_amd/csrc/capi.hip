@@ -96,7 +96,7 @@ const BwdLauncher kDkdv[3][4] = {
 };
 
 // Split-KV decode: range, plan and workspace.
-constexpr int kDecWaves = 4;   // waves per workgroup
+constexpr int kDecWaves = 4;  // waves per workgroup
 constexpr int kDecTile = 32;   // KV rows per tile
 bool decode_applies(const flexatt_problem* p) {
   return (p->dtype == FLEXATT_F16 || p->dtype == FLEXATT_BF16) && p->head_dim <= 128 && !p->doc_bounds &&
