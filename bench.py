@@ -50,8 +50,10 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 10 warm-up steps, then 100 timed: the first steps of a fresh process run a
+    # few percent slower, so short runs understate the steady rate
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="gqa_llama3_8b", choices=sorted(CONFIGS) + sorted(DECODE_CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bounded CPU baseline sample budget")
@@ -97,7 +99,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(attention over (batch, KV-head) groups shards with no communication; see DESIGN.md). "
+              "(attention over (batch, KV-head) groups shards with no communication). "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 

@@ -78,7 +78,7 @@ def document_mask(document_ids: torch.Tensor) -> torch.Tensor:
     """Boolean [B, 1, S, S] mask of pairs in the same document.
 
     Document masking has no counterpart in the reference (it is one of the
-    future candidates it lists, README.md:219; DESIGN.md:374, :382).  Here a
+    future candidates it lists, its README.md:219 and DESIGN.md:374, :382).  Here a
     document is a maximal run of equal values along a row of
     ``document_ids`` [B, S]: positions i and j attend to each other only
     inside one run (on top of the other primitives).

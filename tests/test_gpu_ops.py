@@ -57,6 +57,21 @@ def test_matches_autograd_function(gpu_device, kw):
         check(name, g, r, torch.bfloat16)
 
 
+def test_documents_through_the_operator(gpu_device):
+    _, (q, k, v, do) = _inputs(5, hq=4, hkv=2, sq=90, sk=90, grad=True)
+    ids = torch.tensor([[0] * 30 + [1] * 45 + [2] * 15, [4] * 90], dtype=torch.int32, device=gpu_device)
+    o = flexatt_ops.attention(q, k, v, causal=True, document_ids=ids)
+    o.backward(do)
+    grads = [t.grad.clone() for t in (q, k, v)]
+    for t in (q, k, v):
+        t.grad = None
+    o_ref = nfa.npu_flex_attention(q, k, v, causal=True, document_ids=ids)
+    o_ref.backward(do)
+    assert torch.equal(o, o_ref)
+    for g, t in zip(grads, (q, k, v)):
+        assert torch.equal(g, t.grad)
+
+
 def test_compile_fullgraph(gpu_device):
     torch._dynamo.reset()
     _, (q, k, v, do) = _inputs(4, dtype=torch.float16, grad=True)

@@ -79,3 +79,13 @@ def test_traced_graph_has_single_kernel_nodes():
     gm = make_fx(fn, tracing_mode="fake")(q, k, v)
     targets = [str(n.target) for n in gm.graph.nodes if n.op == "call_function"]
     assert sum("flexatt.fwd" in t for t in targets) == 1, targets
+
+
+def test_meta_autograd_with_documents():
+    q = torch.empty(1, 4, 24, 32, dtype=torch.float16, device="meta", requires_grad=True)
+    k = torch.empty(1, 2, 24, 32, dtype=torch.float16, device="meta", requires_grad=True)
+    v = torch.empty(1, 2, 24, 32, dtype=torch.float16, device="meta", requires_grad=True)
+    doc = torch.empty(1, 24, 2, dtype=torch.int32, device="meta")
+    o, lse = torch.ops.flexatt.fwd(q, k, v, None, 0.2, True, 0, 0.0, doc)
+    o.float().sum().backward()
+    assert o.shape == q.shape and k.grad.shape == k.shape
