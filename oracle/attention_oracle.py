@@ -51,6 +51,7 @@ __all__ = [
     "backward",
     "backward_autograd",
     "forward_backward_chunked",
+    "forward_backward_rows",
     "attention_pairs",
 ]
 
@@ -296,3 +297,63 @@ def forward_backward_chunked(q, k, v, do, causal=False, sliding_window=0, alibi_
             out.append((bi, h, o, lse) + tuple(grads))
             count += 1
     return out
+
+
+def forward_backward_rows(q, k, v, do, causal=False, sliding_window=0, alibi_slope=None, scale=None,
+                          soft_cap=0.0, dtype=torch.float32, chunk=1024):
+    """Forward and closed-form backward of one (batch, KV-head) group,
+    evaluated over chunks of ``chunk`` query rows so that memory stays
+    bounded at full sequence lengths (a [G, chunk, Skv] score block at a
+    time).  Same formulas and results as :func:`forward` + :func:`backward`
+    (``q``, ``do``: [1, G, Sq, D]; ``k``, ``v``: [1, 1, Skv, D]).  Returns
+    (O, LSE, dQ, dK, dV) with dK / dV summed over the G heads.  Each chunk
+    only scores the keys a causal mask or a window leaves to it.
+    """
+    d = q.shape[-1]
+    sc = (1.0 / math.sqrt(d)) if scale is None else float(scale)
+    qf = q.detach().to("cpu", dtype)[0]
+    dof = do.detach().to("cpu", dtype)[0]
+    kf = k.detach().to("cpu", dtype)[0, 0]
+    vf = v.detach().to("cpu", dtype)[0, 0]
+    g, sq, _ = qf.shape
+    skv = kf.shape[0]
+    sl = None if alibi_slope is None else alibi_slope.detach().to("cpu", dtype).view(g, 1, 1)
+    o = torch.empty(g, sq, d, dtype=dtype)
+    lse = torch.empty(g, sq, dtype=dtype)
+    dq = torch.empty(g, sq, d, dtype=dtype)
+    dk = torch.zeros(skv, d, dtype=dtype)
+    dv = torch.zeros(skv, d, dtype=dtype)
+    for r0 in range(0, sq, chunk):
+        r1 = min(sq, r0 + chunk)
+        # keys outside [c0, c1) are masked for every row of the chunk
+        c0 = max(0, r0 - sliding_window) if sliding_window > 0 else 0
+        c1 = min(skv, r1) if causal else skv
+        c1 = max(c1, c0 + 1)  # keep one column so that fully masked rows stay defined
+        i = torch.arange(r0, r1).view(-1, 1)
+        j = torch.arange(c0, c1).view(1, -1)
+        kc, vc = kf[c0:c1], vf[c0:c1]
+        x = torch.matmul(qf[:, r0:r1], kc.transpose(0, 1)) * sc
+        t = None
+        if soft_cap > 0.0:
+            t = torch.tanh(x / soft_cap)
+            x = soft_cap * t
+        if sl is not None:
+            x = x + sl * (i - j).to(dtype)
+        ok = torch.ones(r1 - r0, c1 - c0, dtype=torch.bool)
+        if causal:
+            ok &= j <= i
+        if sliding_window > 0:
+            ok &= (i - j) <= sliding_window
+        p, ls = _softmax_masked(x, ok)
+        oc = torch.matmul(p, vc)
+        o[:, r0:r1] = oc
+        lse[:, r0:r1] = ls
+        dl = (oc * dof[:, r0:r1]).sum(-1, keepdim=True)
+        ds = p * (torch.matmul(dof[:, r0:r1], vc.transpose(0, 1)) - dl)
+        if t is not None:
+            ds = ds * (1.0 - t * t)
+        ds = ds * sc
+        dq[:, r0:r1] = torch.matmul(ds, kc)
+        dk[c0:c1] += torch.matmul(ds.transpose(1, 2), qf[:, r0:r1]).sum(0)
+        dv[c0:c1] += torch.matmul(p.transpose(1, 2), dof[:, r0:r1]).sum(0)
+    return o[None], lse[None], dq[None], dk[None, None], dv[None, None]

@@ -354,3 +354,32 @@ def test_document_backward_closed_form_matches_autograd():
     b = orc.backward_autograd(q, k, v, do, True, 0, None, 0.5, 0.0, document_ids=DOC_IDS)
     for x, y in zip(a, b):
         assert torch.allclose(x, y, atol=1e-11)
+
+
+@pytest.mark.parametrize("causal,window,alibi,cap", [(True, 0, False, 0.0), (True, 3, True, 1.2), (False, 4, False, 0.7)])
+def test_row_chunked_group_equals_full(causal, window, alibi, cap):
+    """forward_backward_rows (query-row chunks, one GQA group) equals the
+    whole-matrix forward + backward, Sq != Skv, chunk not dividing Sq."""
+    q, k, v, do = rnd(1, 3, 13, 8, seed=80), rnd(1, 1, 11, 8, seed=81), rnd(1, 1, 11, 8, seed=82), rnd(1, 3, 13, 8, seed=83)
+    slopes = torch.tensor([0.3, -0.2, 0.5]) if alibi else None
+    o, lse = orc.forward(q, k, v, causal, window, slopes, 0.7, cap)
+    g = orc.backward(q, k, v, do, causal, window, slopes, 0.7, cap)
+    got = orc.forward_backward_rows(q, k, v, do, causal, window, slopes, 0.7, cap, dtype=torch.float64, chunk=5)
+    for x, y in zip(got, (o, lse) + tuple(g)):
+        fin = torch.isfinite(y)
+        assert torch.equal(torch.isfinite(x), fin)
+        assert torch.allclose(x[fin], y[fin], atol=1e-12)
+
+
+def test_row_chunked_group_with_window_skipping_columns():
+    """Chunks whose window excludes leading keys (and causal chunks that stop
+    early) give the whole-matrix result."""
+    q, k, v, do = rnd(1, 2, 40, 8, seed=84), rnd(1, 1, 37, 8, seed=85), rnd(1, 1, 37, 8, seed=86), rnd(1, 2, 40, 8, seed=87)
+    for causal, window in ((True, 6), (False, 9), (True, 0)):
+        o, lse = orc.forward(q, k, v, causal, window, None, 0.5, 0.0)
+        g = orc.backward(q, k, v, do, causal, window, None, 0.5, 0.0)
+        got = orc.forward_backward_rows(q, k, v, do, causal, window, None, 0.5, 0.0, dtype=torch.float64, chunk=7)
+        for x, y in zip(got, (o, lse) + tuple(g)):
+            fin = torch.isfinite(y)
+            assert torch.equal(torch.isfinite(x), fin)
+            assert torch.allclose(x[fin], y[fin], atol=1e-12)
