@@ -70,6 +70,8 @@ Shape make_shape(const flexatt_problem* p) {
   s.window = p->sliding_window;
   s.cap = p->soft_cap;
   s.inv_cap = p->soft_cap > 0.f ? 1.0f / p->soft_cap : 0.f;
+  s.tanh_k = p->soft_cap > 0.f ? 2.0f * kLog2e * p->scale / p->soft_cap : 0.f;
+  s.cap_log2 = p->soft_cap * kLog2e;
   s.alibi = p->alibi_slopes;
   s.doc = p->doc_bounds;
   return s;

@@ -56,6 +56,8 @@ struct Shape {
   int window;         // 0 = off
   float cap;          // 0 = off
   float inv_cap;
+  float tanh_k;       // 2 log2(e) scale / cap: exp2(s * tanh_k) = e^(2 scale s / cap)
+  float cap_log2;     // cap * log2(e)
   const float* alibi;  // [Hq] or nullptr
   const int* doc;      // [B][S][2] document bounds (Sq == Skv = S) or nullptr
 };
@@ -81,12 +83,6 @@ template <class T> __device__ __forceinline__ float to_f32(T x) { return (float)
 // --- small helpers -------------------------------------------------------------
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
-
-// tanh(x) = 1 - 2 / (exp(2x) + 1); saturates correctly at +-inf of exp.
-__device__ __forceinline__ float fast_tanh(float x) {
-  float e = fast_exp2(x * (2.0f * kLog2e));
-  return 1.0f - 2.0f * fast_rcp(e + 1.0f);
-}
 
 // acc *= s in place.  Written with tied asm operands so that a rescale under a
 // branch leaves the accumulator in its registers (a plain multiply makes the
@@ -286,8 +282,11 @@ template <bool SOFTCAP, bool ALIBI>
 __device__ __forceinline__ float score_log2(float s, const Shape& p, float slope_log2, int i, int j, float& t) {
   float y;
   if constexpr (SOFTCAP) {
-    t = fast_tanh(s * p.scale * p.inv_cap);
-    y = t * (p.cap * kLog2e);
+    // tanh(x) = 1 - 2 / (e^(2x) + 1) with x = scale s / cap; y = cap log2(e) tanh(x)
+    // straight from the reciprocal (t is only formed where the caller reads it)
+    const float r = fast_rcp(fast_exp2(s * p.tanh_k) + 1.0f);
+    t = __builtin_fmaf(-2.0f, r, 1.0f);
+    y = __builtin_fmaf(-2.0f * p.cap_log2, r, p.cap_log2);
   } else {
     y = s * p.scale_log2;
   }
