@@ -277,9 +277,10 @@ __device__ __forceinline__ int xcd_remap(int w, int n) {
   return (w & 7) * (n >> 3) + (w >> 3);
 }
 
-// Score transform in the log2 domain for one element: scale, soft-cap, ALiBi.
+// Score transform in the log2 domain for one element: scale, soft-cap, ALiBi
+// (dij = i - j as a float; exact for |i - j| < 2^24).
 template <bool SOFTCAP, bool ALIBI>
-__device__ __forceinline__ float score_log2(float s, const Shape& p, float slope_log2, int i, int j, float& t) {
+__device__ __forceinline__ float score_log2_d(float s, const Shape& p, float slope_log2, float dij, float& t) {
   float y;
   if constexpr (SOFTCAP) {
     // tanh(x) = 1 - 2 / (e^(2x) + 1) with x = scale s / cap; y = cap log2(e) tanh(x)
@@ -290,8 +291,12 @@ __device__ __forceinline__ float score_log2(float s, const Shape& p, float slope
   } else {
     y = s * p.scale_log2;
   }
-  if constexpr (ALIBI) y += slope_log2 * (float)(i - j);
+  if constexpr (ALIBI) y = __builtin_fmaf(slope_log2, dij, y);
   return y;
+}
+template <bool SOFTCAP, bool ALIBI>
+__device__ __forceinline__ float score_log2(float s, const Shape& p, float slope_log2, int i, int j, float& t) {
+  return score_log2_d<SOFTCAP, ALIBI>(s, p, slope_log2, (float)(i - j), t);
 }
 
 // Document bounds [lo, hi) of position s of batch b: the other positions of

@@ -197,13 +197,14 @@ void fwd_mfma_kernel(FwdArgs a) {
 
     // scores -> log2 domain (transform paths), mask (edge tiles only)
     if constexpr (!RAW) {
+      const float fb = (float)(my_m - n0 - 4 * h);  // i - j = fb - (32 bb + 8 (r / 4) + r % 4)
 #pragma unroll
       for (int bb = 0; bb < C::NB; ++bb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
           float tv;
-          s[bb][r] = score_log2<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2, my_m, j, tv);
+          s[bb][r] = score_log2_d<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2,
+                                                 fb - (float)(32 * bb + 8 * (r >> 2) + (r & 3)), tv);
         }
     }
     if (need_mask) {
@@ -356,13 +357,15 @@ void fwd_mfma_kernel(FwdArgs a) {
     tm_lo = __builtin_amdgcn_readfirstlane(tm_lo);
     auto softmax = [&](int n0) {
       if constexpr (!RAW) {
+        // i - j = fb - (32 bb + 8 (r / 4) + r % 4), exact in fp32
+        const float fb = (float)(my_m - n0 - 4 * h);
 #pragma unroll
         for (int bb = 0; bb < C::NB; ++bb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
             float tv;
-            s[bb][r] = score_log2<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2, my_m, j, tv);
+            s[bb][r] = score_log2_d<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2,
+                                                   fb - (float)(32 * bb + 8 * (r >> 2) + (r & 3)), tv);
           }
       }
       const int tn = n0 / C::BN;
