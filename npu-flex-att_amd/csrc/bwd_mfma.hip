@@ -181,13 +181,15 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(BwdArgs a) {
         dp[bb] = M::mma(as_v8<V8>(lds_read16(vr + 16 * kc)), dof[kc], dp[bb]);
       }
     }
+    const float fb = (float)(my_m - n0 - 4 * h);  // i - j = fb - (32 bb + 8 (r / 4) + r % 4), exact
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
         float tv = 0.f;
-        const float y = score_log2<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2, my_m, j, tv);
+        const float y = score_log2_d<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2,
+                                                     fb - (float)(32 * bb + 8 * (r >> 2) + (r & 3)), tv);
         float pr = fast_exp2(y - lse2);
         if (!full && (!allowed(p, my_m, j) || j < dlo || j >= dhi)) pr = 0.f;
         float ds = pr * (dp[bb][r] - dl) * p.scale;
@@ -355,6 +357,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_mfma_kernel(BwdArgs a) {
                         !p.doc;
       const float slope_log2 = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
       const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+      const float fq = (float)(mt + 4 * h - my_n);
 
 #pragma unroll
       for (int mb = 0; mb < C::BMQ / 32; ++mb) {
@@ -392,7 +395,9 @@ __global__ __launch_bounds__(256) void bwd_dkdv_mfma_kernel(BwdArgs a) {
             const int r = 4 * i + j;
             const int m = mt + mr + j;
             float tv = 0.f;
-            const float y = score_log2<SOFTCAP, ALIBI>(s[r], p, slope_log2, m, my_n, tv);
+            // m - my_n = (mt + 4h - my_n) + 32 mb + 8 i + j, exact in fp32
+            const float y = score_log2_d<SOFTCAP, ALIBI>(s[r], p, slope_log2,
+                                                         fq + (float)(32 * mb + 8 * i + j), tv);
             float pr = fast_exp2(y - L[j]);
             if (!full && (!allowed(p, m, my_n) || m < dlo || m >= dhi)) pr = 0.f;
             s[r] = pr;
