@@ -51,11 +51,15 @@ struct BwdCfg {
   // D = 256: dV and dK in two passes over the query tiles (S recomputed), so
   // that the K / V rows and both accumulator sets never share the registers
   static constexpr bool SPLIT = D == 256;
+  // waves per SIMD the register budget targets: two workgroups per CU for
+  // D <= 64 (their VALU work then overlaps the other workgroup's MFMAs)
+  static constexpr int WPE = D <= 64 ? 2 : 1;
 };
 
 // ---------------------------------------------------------------- dQ kernel --
 template <class T, int D, bool SOFTCAP, bool ALIBI>
-__global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(BwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdCfg<D>::WPE, BwdCfg<D>::WPE)))
+void bwd_dq_mfma_kernel(BwdArgs a) {
   using C = BwdCfg<D>;
   using M = Mfma<T>;
   using V8 = typename M::v8;
@@ -229,7 +233,8 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(BwdArgs a) {
 
 // -------------------------------------------------------------- dK/dV kernel --
 template <class T, int D, bool SOFTCAP, bool ALIBI>
-__global__ __launch_bounds__(256) void bwd_dkdv_mfma_kernel(BwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdCfg<D>::WPE, BwdCfg<D>::WPE)))
+void bwd_dkdv_mfma_kernel(BwdArgs a) {
   using C = BwdCfg<D>;
   using M = Mfma<T>;
   using V8 = typename M::v8;
