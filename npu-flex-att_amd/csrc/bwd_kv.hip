@@ -28,8 +28,10 @@
 //    LDS with direct-to-LDS loads four tiles ahead into six stages.
 //  * Step u has two phases separated by workgroup barriers:
 //      M(u): S-wave: the 16 S / dP MFMAs of tile u, with the reads of its
-//            LSE (converted to log2 units) and Delta;  KV-wave: reads the
-//            packed P / dS of tile u-1 and the first transpose reads;
+//            LSE (converted to log2 units) and Delta (the dP MFMAs start
+//            from Delta and run on -V, so they end at Delta - dP and
+//            P (dP - Delta) is one multiply);  KV-wave: reads the packed
+//            P / dS of tile u-1 and the first transpose reads;
 //      V(u): S-wave: P / dS of tile u (VALU), written to the exchange buffer;
 //            KV-wave: the 16 dV / dK MFMAs of tile u-1, then waits for tile
 //            u+1;
@@ -149,7 +151,9 @@ void bwd_kv_kernel(BwdArgs a) {
 #pragma unroll
       for (int kc = 0; kc < C::KC; ++kc) {
         kreg[kc] = as_v8<V8>(ld_global16(kr + 16 * kc));
-        vreg[kc] = as_v8<V8>(ld_global16(vr + 16 * kc));
+        // -V: the dP MFMAs start from Delta and so end at Delta - dP (below)
+        vreg[kc] = as_v8<V8>(ld_global16(vr + 16 * kc) ^ i32x4{(int)0x80008000, (int)0x80008000,
+                                                                (int)0x80008000, (int)0x80008000});
       }
     }
     constexpr bool RAW = !SOFTCAP && !ALIBI;
@@ -161,9 +165,9 @@ void bwd_kv_kernel(BwdArgs a) {
     __syncthreads();  // prologue: tile 0 landed
     for (int u = 0; u <= ntile; ++u) {
       const bool act = u < ntile;
-      f32x16 S, DP;
-      f32x4 L4[4], D4[4];  // LSE (to log2 units) and Delta of this lane's query rows
-      // ---- M(u): S = Q K^T, dP = dO V^T of tile u; LSE / Delta reads ------
+      f32x16 S, DP;        // Q K^T and Delta - dO V^T (the latter accumulated from Delta)
+      f32x4 L4[4];         // LSE (to log2 units) of this lane's query rows
+      // ---- M(u): S = Q K^T, DP = Delta - dO V^T of tile u; LSE reads ------
       if (act) {
         // Row-read addresses of this stage (the Q / dO choice folds into the
         // instruction offset).
@@ -171,22 +175,26 @@ void bwd_kv_kernel(BwdArgs a) {
 #pragma unroll
         for (int kc = 0; kc < C::KC; ++kc) ra[kc] = rowoff[kc] + sc * C::STAGEB;
         auto rdA = [&](int k) { return lds_read16(smem + (ra[k >> 1] + (k & 1) * C::TILEB)); };
+        // Delta of the query rows m0 + 8i + 4h + j is the initial dP
+        // accumulator (element 4i + j), so that P (dP - Delta) needs no
+        // subtraction on the VALU.
+        const float* sR = (const float*)(smem + sc * C::STAGEB + 2 * C::TILEB);
+        f32x4 D4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) D4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 8 + 4 * h));
         i32x4 ab[5];
 #pragma unroll
         for (int k = 0; k < 4; ++k) ab[k] = rdA(k);
         S = f32x16{};
-        DP = f32x16{};
+        DP = f32x16{D4[0][0], D4[0][1], D4[0][2], D4[0][3], D4[1][0], D4[1][1], D4[1][2], D4[1][3],
+                    D4[2][0], D4[2][1], D4[2][2], D4[2][3], D4[3][0], D4[3][1], D4[3][2], D4[3][3]};
 #pragma unroll
         for (int k = 0; k < 2 * C::KC; ++k) {
           __builtin_amdgcn_sched_barrier(0);
           if (k + 4 < 2 * C::KC) ab[(k + 4) % 5] = rdA(k + 4);
           if (k == 8) {  // query rows m0 + 8i + 4h + j
-            const float* sR = (const float*)(smem + sc * C::STAGEB + 2 * C::TILEB);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              L4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 4 * h));
-              D4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 8 + 4 * h));
-            }
+            for (int i = 0; i < 4; ++i) L4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 4 * h));
           }
           if (k >= 12) {  // LSE -> log2 units
             const int i = k - 12;
@@ -244,7 +252,7 @@ void bwd_kv_kernel(BwdArgs a) {
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            float ds = pe[r] * (DP[r] - D4[r >> 2][r & 3]);
+            float ds = -pe[r] * DP[r];  // P (dP - Delta)
             if constexpr (SOFTCAP) ds *= 1.f - tt[r] * tt[r];
             de[r] = ds;
           }
