@@ -154,6 +154,9 @@ def main():
     ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
     # Per-kernel durations through the C ABI, HIP events on the launch stream.
+    # "dq" is flexatt_bwd_dq_delta, the launch the backward makes: for D = 128
+    # fp16/bf16 it also forms Delta (no separate Delta pass), otherwise it is
+    # the Delta pass followed by dQ.
     lib = L.load()
     o, lse = nfa.npu_flash_attention_forward(q, k, v, return_lse=True, **kw)
     delta = torch.empty(B, Hq, Sq, dtype=torch.float32, device=dev)
@@ -166,8 +169,8 @@ def main():
     T = L.tensor
     calls = {
         "fwd": lambda: lib.flexatt_fwd(p, T(q), T(k), T(v), T(o), lse.data_ptr(), sh),
-        "delta": lambda: lib.flexatt_bwd_delta(p, T(o), T(do), delta.data_ptr(), sh),
-        "dq": lambda: lib.flexatt_bwd_dq(p, T(q), T(k), T(v), T(do), lse.data_ptr(), delta.data_ptr(), T(dq), sh),
+        "dq": lambda: lib.flexatt_bwd_dq_delta(p, T(q), T(k), T(v), T(o), T(do), lse.data_ptr(), delta.data_ptr(),
+                                               T(dq), sh),
         "dkdv": lambda: lib.flexatt_bwd_dkdv(p, T(q), T(k), T(v), T(do), lse.data_ptr(), delta.data_ptr(),
                                              T(dk), T(dv), sh),
     }
@@ -185,7 +188,7 @@ def main():
         kernel_ms[name] = statistics.median(a.elapsed_time(b) for a, b in evs)
 
     fwd_ms = kernel_ms["fwd"]
-    bwd_ms = kernel_ms["delta"] + kernel_ms["dq"] + kernel_ms["dkdv"]
+    bwd_ms = kernel_ms["dq"] + kernel_ms["dkdv"]
     fwd_tf = fwd_flop / fwd_ms / 1e9
     bwd_tf = bwd_flop / bwd_ms / 1e9
     total_tf = (fwd_flop + bwd_flop) / ms_step / 1e9

@@ -113,6 +113,16 @@ int flexatt_bwd_dq(const flexatt_problem* p, const flexatt_tensor* q, const flex
                    const flexatt_tensor* v, const flexatt_tensor* dout, const float* lse,
                    const float* delta, const flexatt_tensor* dq, void* stream);
 
+/* Backward Delta and dQ in one pass where the dQ kernel can form Delta itself
+ * (fp16/bf16, head_dim 128, no document mask; otherwise the Delta pass then
+ * dQ): delta (the caller's fp32 [B,Hq,Sq] buffer) receives sum_d o * dout,
+ * for flexatt_bwd_dkdv after it.  Replaces the Delta op and the
+ * flash_attn_bwd_dq_kernel launch of npu_flash_attention_backward,
+ * npu_flash_attention.py:681-712. */
+int flexatt_bwd_dq_delta(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                         const flexatt_tensor* v, const flexatt_tensor* o, const flexatt_tensor* dout,
+                         const float* lse, float* delta, const flexatt_tensor* dq, void* stream);
+
 /* Backward dK/dV with the GQA group sum folded in: dk/dv are [B, Hkv, Skv, D].
  * Replaces the flash_attn_bwd_dkdv_kernel launch plus the group sum,
  * npu_flash_attention.py:714-737. */
@@ -121,8 +131,8 @@ int flexatt_bwd_dkdv(const flexatt_problem* p, const flexatt_tensor* q, const fl
                      const float* delta, const flexatt_tensor* dk, const flexatt_tensor* dv,
                      void* stream);
 
-/* Whole backward: delta (into the caller's fp32 [B,Hq,Sq] `delta` buffer),
- * then dQ, then dK/dV.  Replaces the kernel launches and torch ops of
+/* Whole backward: delta (into the caller's fp32 [B,Hq,Sq] `delta` buffer)
+ * and dQ (flexatt_bwd_dq_delta), then dK/dV.  Replaces the kernel launches and torch ops of
  * npu_flash_attention_backward, npu_flash_attention.py:659-739. */
 int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
                 const flexatt_tensor* v, const flexatt_tensor* o, const flexatt_tensor* dout,
@@ -135,7 +145,7 @@ const char* flexatt_status_string(int status);
 /* ABI version of this header (bumped on any signature change). */
 int flexatt_abi_version(void);
 
-#define FLEXATT_ABI_VERSION 3
+#define FLEXATT_ABI_VERSION 4
 
 #ifdef __cplusplus
 }

@@ -27,6 +27,11 @@
 //  * K / V tiles are copied global -> LDS with direct-to-LDS loads two tiles
 //    ahead into four stages, issued in the VALU phases; every phase ends with
 //    a workgroup barrier.
+//  * Fused Delta (a.delta_out set): each wave also loads its O rows with the
+//    Q / dO rows and forms Delta = sum_d O dO of its rows itself (fp32, a
+//    fixed order); the first wave of each pair writes it for the dK/dV
+//    kernel, so the separate Delta pass (npu_flash_attention.py:681-685) is
+//    not launched.
 // Deterministic: every output element is owned by one lane pair and
 // accumulated in a fixed order.
 #include "flexatt_device.h"
@@ -107,7 +112,15 @@ void bwd_q_kernel(BwdArgs a) {
     }
     const int64_t rr = (int64_t)(b * p.Hq + hq) * p.Sq + r;
     lse2 = a.lse[rr] * kLog2e;
-    dlt = a.delta[rr];
+    i32x4 orow[C::KC];
+    if (a.delta_out) {
+      const T* ob = (const T*)a.o.data + b * a.o.sb + hq * a.o.sh + (int64_t)r * a.o.ss + 8 * h;
+#pragma unroll
+      for (int kc = 0; kc < C::KC; ++kc) orow[kc] = ld_global16(ob + 16 * kc);
+      dlt = 0.f;
+    } else {
+      dlt = a.delta[rr];
+    }
     // a row with no allowed key (LSE = -inf) contributes nothing: every one of
     // its pairs is masked, and +inf makes exp2(y - lse2) = 0 for those
     if (!(lse2 > kNegInf)) lse2 = kPosInf;
@@ -115,6 +128,23 @@ void bwd_q_kernel(BwdArgs a) {
     // vmcnt(0) wait at their first use inside the tile loop, which would also
     // drain the tile copies in flight on every tile.
     wait_vmcnt<0>();
+    if (a.delta_out) {
+      // Delta of this lane's row: its half (8 h + 16 kc + t) in fp32, then the
+      // other half from lane l ^ 32.
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int kc = 0; kc < C::KC; ++kc) {
+        const V8 ov = as_v8<V8>(orow[kc]);
+#pragma unroll
+        for (int t = 0; t < 8; t += 2) {
+          s0 = __builtin_fmaf(to_f32(ov[t]), to_f32(df[kc][t]), s0);
+          s1 = __builtin_fmaf(to_f32(ov[t + 1]), to_f32(df[kc][t + 1]), s1);
+        }
+      }
+      const float half = s0 + s1;
+      dlt = half + swap_halves(half);
+      if (grp == 0 && h == 0 && my_m < p.Sq) a.delta_out[rr] = dlt;
+    }
 #pragma unroll
     for (int kc = 0; kc < C::KC; ++kc) {
       pin(qf[kc]);

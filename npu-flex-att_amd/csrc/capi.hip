@@ -140,6 +140,10 @@ BwdLauncher pick_dq(const flexatt_problem* p) {
     return p->dtype == FLEXATT_BF16 ? bwd_dq_mfma_bf16_d128 : bwd_dq_mfma_f16_d128;
   return kDq[p->dtype][head_index(p->head_dim)];
 }
+// The dQ kernel that can also form Delta itself (the D = 128 tile stream).
+bool dq_fuses_delta(const flexatt_problem* p) {
+  return pick_dq(p) == (p->dtype == FLEXATT_BF16 ? bwd_q_bf16_d128 : bwd_q_f16_d128);
+}
 BwdLauncher pick_dkdv(const flexatt_problem* p) {
   if (p->doc_bounds && p->head_dim == 128 && p->dtype != FLEXATT_F32)
     return p->dtype == FLEXATT_BF16 ? bwd_dkdv_mfma_bf16_d128 : bwd_dkdv_mfma_f16_d128;
@@ -169,6 +173,8 @@ int bwd_common(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_
   a.delta = delta;
   a.p = make_shape(p);
   a.ntiles = 0;
+  a.o = View{nullptr, 0, 0, 0};
+  a.delta_out = nullptr;
   return FLEXATT_OK;
 }
 
@@ -272,6 +278,24 @@ int flexatt_bwd_dq(const flexatt_problem* p, const flexatt_tensor* q, const flex
   return (int)pick_dq(p)(a, (hipStream_t)stream);
 }
 
+int flexatt_bwd_dq_delta(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                         const flexatt_tensor* v, const flexatt_tensor* o, const flexatt_tensor* dout,
+                         const float* lse, float* delta, const flexatt_tensor* dq, void* stream) {
+  BwdArgs a;
+  FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
+  FLEXATT_TRY(check_tensor(o, p->dtype));
+  FLEXATT_TRY(check_tensor(dq, p->dtype));
+  if (!dq_fuses_delta(p)) {  // Delta pass, then dQ
+    FLEXATT_TRY(flexatt_bwd_delta(p, o, dout, delta, stream));
+    a.dq = mview(dq);
+    return (int)pick_dq(p)(a, (hipStream_t)stream);
+  }
+  a.o = view(o);
+  a.delta_out = delta;
+  a.dq = mview(dq);
+  return (int)pick_dq(p)(a, (hipStream_t)stream);
+}
+
 int flexatt_bwd_dkdv(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
                      const flexatt_tensor* v, const flexatt_tensor* dout, const float* lse,
                      const float* delta, const flexatt_tensor* dk, const flexatt_tensor* dv,
@@ -295,12 +319,9 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
   FLEXATT_TRY(check_tensor(dq, p->dtype));
   FLEXATT_TRY(check_tensor(dk, p->dtype));
   FLEXATT_TRY(check_tensor(dv, p->dtype));
-  FLEXATT_TRY(flexatt_bwd_delta(p, o, dout, delta, stream));
-  a.dq = mview(dq);
+  FLEXATT_TRY(flexatt_bwd_dq_delta(p, q, k, v, o, dout, lse, delta, dq, stream));
   a.dk = mview(dk);
   a.dv = mview(dv);
-  const int hi = head_index(p->head_dim);
-  FLEXATT_TRY((int)pick_dq(p)(a, (hipStream_t)stream));
   return (int)pick_dkdv(p)(a, (hipStream_t)stream);
 }
 

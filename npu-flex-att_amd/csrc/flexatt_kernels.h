@@ -28,6 +28,10 @@ struct BwdArgs {
   MutView dq, dk, dv;
   Shape p;
   int ntiles;  // number of row tiles of the kernel's grid (set by the launcher)
+  // dQ with Delta computed in the kernel (bwd_q only): O, and where Delta is
+  // written for the dK/dV kernel; delta_out == nullptr: Delta is read from delta.
+  View o;
+  float* delta_out;
 };
 
 // Split-KV decode forward (fwd_decode.hip): partials in the caller's workspace.
@@ -78,7 +82,8 @@ hipError_t fwd_decode_f16_d128(const DecodeArgs&, hipStream_t);
 hipError_t bwd_kv_bf16_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_f16_d128(const BwdArgs&, hipStream_t);
 
-// dQ as a query-stationary tile stream (bwd_q.hip), D = 128.
+// dQ as a query-stationary tile stream (bwd_q.hip), D = 128; with
+// a.delta_out set it also computes Delta (written there) from O and dO.
 hipError_t bwd_q_bf16_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_q_f16_d128(const BwdArgs&, hipStream_t);
 

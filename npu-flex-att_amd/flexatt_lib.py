@@ -21,12 +21,13 @@ EXPORTS = (
     "flexatt_fwd_decode",
     "flexatt_bwd_delta",
     "flexatt_bwd_dq",
+    "flexatt_bwd_dq_delta",
     "flexatt_bwd_dkdv",
     "flexatt_bwd",
     "flexatt_status_string",
     "flexatt_abi_version",
 )
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class Tensor(ctypes.Structure):
@@ -87,6 +88,7 @@ def load() -> ctypes.CDLL:
         "flexatt_fwd_decode": [pr, T, T, T, T, fp, fp, ctypes.c_size_t, st],
         "flexatt_bwd_delta": [pr, T, T, fp, st],
         "flexatt_bwd_dq": [pr, T, T, T, T, fp, fp, T, st],
+        "flexatt_bwd_dq_delta": [pr, T, T, T, T, T, fp, fp, T, st],
         "flexatt_bwd_dkdv": [pr, T, T, T, T, fp, fp, T, T, st],
         "flexatt_bwd": [pr, T, T, T, T, T, fp, fp, T, T, T, st],
     }

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_status_strings():
     lib = L.load()
     assert lib.flexatt_abi_version() == L.ABI_VERSION
-    assert b"#define FLEXATT_ABI_VERSION 3" in open(HEADER, "rb").read()
+    assert b"#define FLEXATT_ABI_VERSION 4" in open(HEADER, "rb").read()
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.flexatt_status_string(code)
     assert b"head_dim" in lib.flexatt_status_string(-3)
