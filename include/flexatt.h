@@ -21,7 +21,9 @@
  *    log-sum-exp of the masked, scaled (and soft-capped, ALiBi-biased) scores.
  *  - All work is enqueued on `stream` (a hipStream_t; NULL = the null
  *    stream) and is asynchronous.  Nothing is allocated or freed: the caller
- *    owns every buffer.  Results are bitwise deterministic.
+ *    owns every buffer (flexatt_fwd_decode_noalloc alone uses a fixed
+ *    library-owned device buffer instead of a workspace argument).  Results
+ *    are bitwise deterministic.
  *  - Return value: FLEXATT_OK, a negative FLEXATT_E* code for a rejected
  *    argument (nothing is launched), or a positive hipError_t from a launch.
  */
@@ -46,7 +48,8 @@ enum flexatt_status {
   FLEXATT_EHEADDIM = -3,   /* head_dim not in {32, 64, 128, 256} */
   FLEXATT_ESHAPE = -4,     /* heads_q % heads_kv != 0, or sizes overflow */
   FLEXATT_ELAYOUT = -5,    /* innermost stride != 1 or a row not 16-byte aligned */
-  FLEXATT_ERANGE = -6      /* problem outside an entry point's range (see its comment) */
+  FLEXATT_ERANGE = -6,     /* problem outside an entry point's range (see its comment) */
+  FLEXATT_ESCRATCH = -7    /* problem needs more than the fixed scratch buffer of a no-alloc entry point */
 };
 
 /* One [B, H, S, D] tensor: device pointer and element strides. */
@@ -101,6 +104,24 @@ size_t flexatt_fwd_decode_workspace(const flexatt_problem* p); /* 0: outside the
 int flexatt_fwd_decode(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
                        const flexatt_tensor* v, const flexatt_tensor* o, float* lse, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/* Split-KV decode forward that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory or pass a
+ * workspace (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same kernels, split plan and results as
+ * flexatt_fwd_decode (bitwise equal), with the partial results in a
+ * library-owned device buffer of FLEXATT_NOALLOC_SCRATCH_BYTES per GPU,
+ * held until the process ends; nothing is allocated or freed per call.
+ * Range: that of flexatt_fwd_decode (else FLEXATT_ERANGE), and
+ * flexatt_fwd_decode_workspace(p) <= FLEXATT_NOALLOC_SCRATCH_BYTES (else
+ * FLEXATT_ESCRATCH, checked before any GPU work).  `stream` must belong to
+ * the current device.  Every call on one GPU shares that GPU's buffer:
+ * calls that overlap on one GPU (on different streams or host threads)
+ * race, so the caller serialises them; calls in order on one stream are
+ * safe (each one overwrites every partial it reads). */
+#define FLEXATT_NOALLOC_SCRATCH_BYTES (16u << 20)
+int flexatt_fwd_decode_noalloc(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                               const flexatt_tensor* v, const flexatt_tensor* o, float* lse, void* stream);
 
 /* Backward pre-pass: delta[b,h,i] = sum_d o * dout in fp32.
  * Replaces the torch op at npu_flash_attention.py:681-685. */

@@ -3,6 +3,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/flexatt.h"
 #include "flexatt_kernels.h"
 
@@ -133,6 +135,61 @@ const DecodeLauncher kDecode[3][3] = {
     {fwd_decode_bf16_d32, fwd_decode_bf16_d64, fwd_decode_bf16_d128},
 };
 
+// Launch the decode kernels with their partials in `ws` (d.bytes, 16-byte
+// aligned); the problem and tensors are already checked.
+int decode_run(const flexatt_problem* p, const DecodePlan& d, const flexatt_tensor* q, const flexatt_tensor* k,
+               const flexatt_tensor* v, const flexatt_tensor* o, float* lse, void* ws, hipStream_t stream) {
+  DecodeArgs a;
+  a.q = view(q);
+  a.k = view(k);
+  a.v = view(v);
+  a.o = mview(o);
+  a.lse = lse;
+  a.p = make_shape(p);
+  a.nsplit = d.nsplit;
+  a.chunk = d.chunk;
+  a.ntiles = d.ntiles;
+  const int64_t rows = (int64_t)p->batch * p->heads_q * p->seqlen_q;
+  a.part_o = (float*)ws;
+  a.part_lse = a.part_o + rows * d.nsplit * p->head_dim;
+  return (int)kDecode[p->dtype][head_index(p->head_dim)](a, stream);
+}
+
+// Fixed partial-result buffer of flexatt_fwd_decode_noalloc: one copy per GPU,
+// held until the process ends.  Host code never passes the name `scratch`
+// itself to a kernel (on the host it is a stand-in, not a device address):
+// the device address of each GPU's copy is looked up once, with that GPU
+// current, and kept in scratch_ptr.
+static __device__ __align__(256) unsigned char scratch[FLEXATT_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[kMaxDevices] = {};
+
+// Device address of the scratch copy of the GPU that `stream` runs on, which
+// must be the current device (the lookup needs it current).
+int scratch_for_stream(hipStream_t stream, void** out) {
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return (int)e;
+  if (stream) {
+    int sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return (int)e;
+    if (sdev != cur) return FLEXATT_EINVAL;
+  }
+  if (cur < 0 || cur >= kMaxDevices) return FLEXATT_EINVAL;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[cur]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!ptr) return (int)hipErrorInvalidSymbol;
+    scratch_ptr[cur] = ptr;
+  }
+  *out = scratch_ptr[cur];
+  return FLEXATT_OK;
+}
+
 // Document masks run on the general backward kernels (the D = 128 tile
 // streams have no document bounds).
 BwdLauncher pick_dq(const flexatt_problem* p) {
@@ -193,6 +250,7 @@ const char* flexatt_status_string(int status) {
     case FLEXATT_ESHAPE: return "inconsistent shape (heads_q % heads_kv != 0 or sizes overflow)";
     case FLEXATT_ELAYOUT: return "unsupported layout (innermost stride != 1 or rows not 16-byte aligned)";
     case FLEXATT_ERANGE: return "problem outside the entry point's range";
+    case FLEXATT_ESCRATCH: return "problem needs more than the library's fixed scratch buffer (FLEXATT_NOALLOC_SCRATCH_BYTES)";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown flexatt status";
   }
 }
@@ -234,21 +292,26 @@ int flexatt_fwd_decode(const flexatt_problem* p, const flexatt_tensor* q, const 
   const DecodePlan d = decode_plan(p);
   if (workspace_bytes < d.bytes) return FLEXATT_EINVAL;
   if (((uintptr_t)workspace) % 16 != 0) return FLEXATT_ELAYOUT;
-  DecodeArgs a;
-  a.q = view(q);
-  a.k = view(k);
-  a.v = view(v);
-  a.o = mview(o);
-  a.lse = lse;
-  a.p = make_shape(p);
-  a.nsplit = d.nsplit;
-  a.chunk = d.chunk;
-  a.ntiles = d.ntiles;
-  const int64_t rows = (int64_t)p->batch * p->heads_q * p->seqlen_q;
-  a.part_o = (float*)workspace;
-  a.part_lse = a.part_o + rows * d.nsplit * p->head_dim;
   if (d.ntiles == 0) return FLEXATT_EINVAL;
-  return (int)kDecode[p->dtype][head_index(p->head_dim)](a, (hipStream_t)stream);
+  return decode_run(p, d, q, k, v, o, lse, workspace, (hipStream_t)stream);
+}
+
+int flexatt_fwd_decode_noalloc(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                               const flexatt_tensor* v, const flexatt_tensor* o, float* lse, void* stream) {
+  FLEXATT_TRY(check_problem(p));
+  FLEXATT_TRY(check_tensor(q, p->dtype));
+  FLEXATT_TRY(check_tensor(k, p->dtype));
+  FLEXATT_TRY(check_tensor(v, p->dtype));
+  FLEXATT_TRY(check_tensor(o, p->dtype));
+  if (!lse) return FLEXATT_EINVAL;
+  if (!decode_applies(p)) return FLEXATT_ERANGE;
+  const DecodePlan d = decode_plan(p);
+  if (d.ntiles == 0) return FLEXATT_EINVAL;
+  // sizes are checked before anything touches the GPU
+  if (d.bytes > (size_t)FLEXATT_NOALLOC_SCRATCH_BYTES) return FLEXATT_ESCRATCH;
+  void* ws = nullptr;
+  FLEXATT_TRY(scratch_for_stream((hipStream_t)stream, &ws));
+  return decode_run(p, d, q, k, v, o, lse, ws, (hipStream_t)stream);
 }
 
 int flexatt_bwd_delta(const flexatt_problem* p, const flexatt_tensor* o, const flexatt_tensor* dout,

@@ -19,6 +19,7 @@ EXPORTS = (
     "flexatt_fwd",
     "flexatt_fwd_decode_workspace",
     "flexatt_fwd_decode",
+    "flexatt_fwd_decode_noalloc",
     "flexatt_bwd_delta",
     "flexatt_bwd_dq",
     "flexatt_bwd_dq_delta",
@@ -28,6 +29,8 @@ EXPORTS = (
     "flexatt_abi_version",
 )
 ABI_VERSION = 4
+# Fixed scratch of flexatt_fwd_decode_noalloc (FLEXATT_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 
 class Tensor(ctypes.Structure):
@@ -86,6 +89,7 @@ def load() -> ctypes.CDLL:
     sig = {
         "flexatt_fwd": [pr, T, T, T, T, fp, st],
         "flexatt_fwd_decode": [pr, T, T, T, T, fp, fp, ctypes.c_size_t, st],
+        "flexatt_fwd_decode_noalloc": [pr, T, T, T, T, fp, st],
         "flexatt_bwd_delta": [pr, T, T, fp, st],
         "flexatt_bwd_dq": [pr, T, T, T, T, fp, fp, T, st],
         "flexatt_bwd_dq_delta": [pr, T, T, T, T, T, fp, fp, T, st],
