@@ -48,6 +48,12 @@ int check_problem(const flexatt_problem* p) {
   return FLEXATT_OK;
 }
 
+#define FLEXATT_TRY_OK(x)               \
+  do {                                  \
+    const int rc_ = (x);                \
+    if (rc_ != FLEXATT_OK) return rc_;  \
+  } while (0)
+
 int check_tensor(const flexatt_tensor* t, int dt) {
   if (!t || !t->data) return FLEXATT_EINVAL;
   const int64_t es = (int64_t)elt_size(dt);
@@ -55,6 +61,33 @@ int check_tensor(const flexatt_tensor* t, int dt) {
   if (t->stride_b < 0 || t->stride_h < 0 || t->stride_s < 0) return FLEXATT_ELAYOUT;
   if (((uintptr_t)t->data) % 16 != 0) return FLEXATT_ELAYOUT;
   if ((t->stride_b * es) % 16 || (t->stride_h * es) % 16 || (t->stride_s * es) % 16) return FLEXATT_ELAYOUT;
+  return FLEXATT_OK;
+}
+
+// Output tensors: the input rules, and no two elements of the [b, h, s, d]
+// index space may share an address (several workgroups would store to it,
+// and the results would depend on their order).  Sufficient test: over the
+// dimensions of extent > 1 sorted by stride, each stride exceeds the span of
+// the smaller ones.
+int check_out_tensor(const flexatt_tensor* t, int dt, int64_t n_b, int64_t n_h, int64_t n_s, int64_t n_d) {
+  FLEXATT_TRY_OK(check_tensor(t, dt));
+  int64_t st[4] = {t->stride_b, t->stride_h, t->stride_s, 1};
+  int64_t ext[4] = {n_b, n_h, n_s, n_d};
+  int order[4], n = 0;
+  for (int i = 0; i < 4; ++i)
+    if (ext[i] > 1) order[n++] = i;
+  for (int i = 1; i < n; ++i)  // insertion sort by stride
+    for (int j = i; j > 0 && st[order[j]] < st[order[j - 1]]; --j) {
+      const int x = order[j];
+      order[j] = order[j - 1];
+      order[j - 1] = x;
+    }
+  int64_t span = 0;  // largest offset reachable with the dims sorted so far
+  for (int i = 0; i < n; ++i) {
+    const int d = order[i];
+    if (st[d] <= span) return FLEXATT_ELAYOUT;
+    span += (ext[d] - 1) * st[d];
+  }
   return FLEXATT_OK;
 }
 
@@ -261,7 +294,7 @@ int flexatt_fwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
   FLEXATT_TRY(check_tensor(q, p->dtype));
   FLEXATT_TRY(check_tensor(k, p->dtype));
   FLEXATT_TRY(check_tensor(v, p->dtype));
-  FLEXATT_TRY(check_tensor(o, p->dtype));
+  FLEXATT_TRY(check_out_tensor(o, p->dtype, p->batch, p->heads_q, p->seqlen_q, p->head_dim));
   if (!lse) return FLEXATT_EINVAL;
   FwdArgs a;
   a.q = view(q);
@@ -286,7 +319,7 @@ int flexatt_fwd_decode(const flexatt_problem* p, const flexatt_tensor* q, const 
   FLEXATT_TRY(check_tensor(q, p->dtype));
   FLEXATT_TRY(check_tensor(k, p->dtype));
   FLEXATT_TRY(check_tensor(v, p->dtype));
-  FLEXATT_TRY(check_tensor(o, p->dtype));
+  FLEXATT_TRY(check_out_tensor(o, p->dtype, p->batch, p->heads_q, p->seqlen_q, p->head_dim));
   if (!lse || !workspace) return FLEXATT_EINVAL;
   if (!decode_applies(p)) return FLEXATT_ERANGE;
   const DecodePlan d = decode_plan(p);
@@ -302,7 +335,7 @@ int flexatt_fwd_decode_noalloc(const flexatt_problem* p, const flexatt_tensor* q
   FLEXATT_TRY(check_tensor(q, p->dtype));
   FLEXATT_TRY(check_tensor(k, p->dtype));
   FLEXATT_TRY(check_tensor(v, p->dtype));
-  FLEXATT_TRY(check_tensor(o, p->dtype));
+  FLEXATT_TRY(check_out_tensor(o, p->dtype, p->batch, p->heads_q, p->seqlen_q, p->head_dim));
   if (!lse) return FLEXATT_EINVAL;
   if (!decode_applies(p)) return FLEXATT_ERANGE;
   const DecodePlan d = decode_plan(p);
@@ -336,7 +369,7 @@ int flexatt_bwd_dq(const flexatt_problem* p, const flexatt_tensor* q, const flex
                    const float* delta, const flexatt_tensor* dq, void* stream) {
   BwdArgs a;
   FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
-  FLEXATT_TRY(check_tensor(dq, p->dtype));
+  FLEXATT_TRY(check_out_tensor(dq, p->dtype, p->batch, p->heads_q, p->seqlen_q, p->head_dim));
   a.dq = mview(dq);
   return (int)pick_dq(p)(a, (hipStream_t)stream);
 }
@@ -347,7 +380,7 @@ int flexatt_bwd_dq_delta(const flexatt_problem* p, const flexatt_tensor* q, cons
   BwdArgs a;
   FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
   FLEXATT_TRY(check_tensor(o, p->dtype));
-  FLEXATT_TRY(check_tensor(dq, p->dtype));
+  FLEXATT_TRY(check_out_tensor(dq, p->dtype, p->batch, p->heads_q, p->seqlen_q, p->head_dim));
   if (!dq_fuses_delta(p)) {  // Delta pass, then dQ
     FLEXATT_TRY(flexatt_bwd_delta(p, o, dout, delta, stream));
     a.dq = mview(dq);
@@ -365,8 +398,8 @@ int flexatt_bwd_dkdv(const flexatt_problem* p, const flexatt_tensor* q, const fl
                      void* stream) {
   BwdArgs a;
   FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
-  FLEXATT_TRY(check_tensor(dk, p->dtype));
-  FLEXATT_TRY(check_tensor(dv, p->dtype));
+  FLEXATT_TRY(check_out_tensor(dk, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
+  FLEXATT_TRY(check_out_tensor(dv, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
   a.dk = mview(dk);
   a.dv = mview(dv);
   return (int)pick_dkdv(p)(a, (hipStream_t)stream);
@@ -379,9 +412,9 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
   BwdArgs a;
   FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
   FLEXATT_TRY(check_tensor(o, p->dtype));
-  FLEXATT_TRY(check_tensor(dq, p->dtype));
-  FLEXATT_TRY(check_tensor(dk, p->dtype));
-  FLEXATT_TRY(check_tensor(dv, p->dtype));
+  FLEXATT_TRY(check_out_tensor(dq, p->dtype, p->batch, p->heads_q, p->seqlen_q, p->head_dim));
+  FLEXATT_TRY(check_out_tensor(dk, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
+  FLEXATT_TRY(check_out_tensor(dv, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
   FLEXATT_TRY(flexatt_bwd_dq_delta(p, q, k, v, o, dout, lse, delta, dq, stream));
   a.dk = mview(dk);
   a.dv = mview(dv);

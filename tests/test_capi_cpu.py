@@ -132,3 +132,86 @@ def test_decode_rejections():
     assert lib.flexatt_fwd_decode(p, t, t, t, t, None, FAKE, need, None) == -1
     assert lib.flexatt_fwd_decode(p, t, t, t, t, FAKE, FAKE + 8, need, None) == -5
     assert lib.flexatt_fwd_decode(p, t, t, t, tens(stride_d=2), FAKE, FAKE, need, None) == -5
+
+
+@pytest.mark.parametrize("entry", ["fwd", "dq", "dkdv"])
+def test_overlapping_outputs_rejected(entry):
+    """An output whose elements share addresses (a zero or too-small stride)
+    is refused: several workgroups would store to one address."""
+    lib = L.load()
+    good = tens()
+    p = problem(batch=2)
+    for bad in (tens(stride_h=0), tens(stride_s=0), tens(stride_b=0), tens(stride_s=32), tens(stride_h=64 * 63)):
+        if entry == "fwd":
+            rc = lib.flexatt_fwd(p, good, good, good, bad, FAKE, None)
+        elif entry == "dq":
+            rc = lib.flexatt_bwd_dq(p, good, good, good, good, FAKE, FAKE, bad, None)
+        else:
+            rc = lib.flexatt_bwd_dkdv(p, good, good, good, good, FAKE, FAKE, good, bad, None)
+        assert rc == -5, (entry, bad.stride_b, bad.stride_h, bad.stride_s)
+
+
+def test_outputs_with_unit_extent_or_permuted_strides_pass_the_layout_check():
+    """A zero stride over an extent-1 dimension, and a [B, S, H, D] storage
+    order, are not overlaps: these calls get past the layout checks (and then
+    stop at the null lse pointer, before any launch)."""
+    lib = L.load()
+    good = tens()
+    p = problem(batch=1)
+    assert lib.flexatt_fwd(p, good, good, good, tens(stride_b=0), None, None) == -1
+    bsnd = tens(stride_b=64 * 4 * 64, stride_h=64, stride_s=4 * 64)
+    assert lib.flexatt_fwd(p, good, good, good, bsnd, None, None) == -1
+
+
+def _integration_stub():
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    blocks = re.findall(r"```python\n(.*?)```", text, re.S)
+    stubs = [b for b in blocks if "class FlexProblem" in b]
+    assert len(stubs) == 1, "INTEGRATION.md should hold one ctypes stub"
+    return stubs[0]
+
+
+def test_integration_stub_matches_the_abi(monkeypatch):
+    """The reference-side binding documented in INTEGRATION.md runs against
+    the built library (it checks the ABI version itself) and its structs have
+    the header's size and field offsets."""
+    monkeypatch.setenv("FLEXATT_LIB", L.LIB_PATH)
+    L.load()
+    ns = {}
+    exec(compile(_integration_stub(), "INTEGRATION.md", "exec"), ns)
+    assert ns["_ABI"] == L.ABI_VERSION
+    for stub, ours in ((ns["FlexProblem"], L.Problem), (ns["FlexTensor"], L.Tensor)):
+        assert ctypes.sizeof(stub) == ctypes.sizeof(ours)
+        assert [f[0] for f in stub._fields_] == [f[0] for f in ours._fields_]
+        for name, _ in ours._fields_:
+            assert getattr(stub, name).offset == getattr(ours, name).offset, name
+    assert ctypes.sizeof(ns["FlexProblem"]) == 64 and ns["FlexProblem"].doc_bounds.offset == 56
+
+
+def test_header_struct_layout_compiled(tmp_path):
+    """sizeof / offsetof of the header's structs, compiled with the host C
+    compiler, equal the ctypes layout of the Python binding."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "flexatt.h"\n'
+        "#define F(s, m) printf(#m \" %zu\\n\", offsetof(s, m));\n"
+        "int main(void) {\n"
+        '  printf("problem %zu\\n", sizeof(flexatt_problem));\n'
+        '  printf("tensor %zu\\n", sizeof(flexatt_tensor));\n'
+        + "".join(f"  F(flexatt_problem, {f[0]})\n" for f in L.Problem._fields_)
+        + "".join(f"  F(flexatt_tensor, {f[0]})\n" for f in L.Tensor._fields_)
+        + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-std=c99", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    vals = [int(line.split()[1]) for line in out if line]
+    assert vals[0] == ctypes.sizeof(L.Problem) and vals[1] == ctypes.sizeof(L.Tensor)
+    want = [getattr(L.Problem, f[0]).offset for f in L.Problem._fields_] + \
+           [getattr(L.Tensor, f[0]).offset for f in L.Tensor._fields_]
+    assert vals[2:] == want
