@@ -3,7 +3,9 @@
 Workload (the north-star configuration): bf16 causal
 GQA, B=2 Hq=32 Hkv=8 D=128 S=4096, synthetic N(0,1) inputs already resident
 in HBM.  One step = forward (O, LSE) + backward (Delta, dQ, dK/dV), exactly
-what npu_flash_attention_forward + npu_flash_attention_backward launch.
+what npu_flash_attention_forward + npu_flash_attention_backward launch
+(for head_dim 128 fp16/bf16 the backward stages dS through a workspace:
+Delta pass, dK/dV writing dS, dQ = dS K).
 
 FLOP convention: fwd = 4*D*N_pairs*B*Hq over attended (i, j) pairs only,
 bwd = 2.5 * fwd (recomputation not counted).  Peak = 2516.6 TFLOP/s
@@ -60,6 +62,8 @@ def parse():
     ap.add_argument("--layout", default="bnsd", choices=("bnsd", "bsnd"),
                     help="storage of Q/K/V/dO (and so O, dQ, dK, dV): [B,H,S,D], or [B,S,H,D] passed as strided views")
     ap.add_argument("--no-gemm-peak", action="store_true", help="skip the plain bf16 GEMM reference rate")
+    ap.add_argument("--recompute-dq", action="store_true",
+                    help="backward without dS staging: the dQ kernel recomputes S and dP (flexatt_bwd)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one 256 MiB device copy (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -114,6 +118,7 @@ def main():
     dev = torch.device("cuda:0")
     if args.config in DECODE_CONFIGS:
         return decode_main(args, dev)
+    nfa.ds_staging_enabled = not args.recompute_dq
     B, Hq, Hkv, Sq, Skv, D, dts, causal, window, cap, alibi, scale, insc = CONFIGS[args.config]
     dtype = {"bf16": torch.bfloat16, "fp16": torch.float16}[dts]
     g = torch.Generator().manual_seed(42)
@@ -153,10 +158,11 @@ def main():
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
-    # Per-kernel durations through the C ABI, HIP events on the launch stream.
-    # "dq" is flexatt_bwd_dq_delta, the launch the backward makes: for D = 128
-    # fp16/bf16 it also forms Delta (no separate Delta pass), otherwise it is
-    # the Delta pass followed by dQ.
+    # Per-kernel durations through the C ABI, HIP events on the launch stream,
+    # of the launches the backward makes.  With dS staging (head_dim 128
+    # fp16/bf16): the Delta pass, dK/dV (which also writes dS) and dQ = dS K.
+    # Otherwise: "dq" is flexatt_bwd_dq_delta (the Delta pass, then the dQ
+    # kernel that recomputes S and dP) and "dkdv" the dK/dV kernel.
     lib = L.load()
     o, lse = nfa.npu_flash_attention_forward(q, k, v, return_lse=True, **kw)
     delta = torch.empty(B, Hq, Sq, dtype=torch.float32, device=dev)
@@ -167,13 +173,19 @@ def main():
     st = torch.cuda.current_stream(dev)
     sh = st.cuda_stream
     T = L.tensor
-    calls = {
-        "fwd": lambda: lib.flexatt_fwd(p, T(q), T(k), T(v), T(o), lse.data_ptr(), sh),
-        "dq": lambda: lib.flexatt_bwd_dq_delta(p, T(q), T(k), T(v), T(o), T(do), lse.data_ptr(), delta.data_ptr(),
-                                               T(dq), sh),
-        "dkdv": lambda: lib.flexatt_bwd_dkdv(p, T(q), T(k), T(v), T(do), lse.data_ptr(), delta.data_ptr(),
-                                             T(dk), T(dv), sh),
-    }
+    ws_bytes = lib.flexatt_bwd_workspace(p) if nfa.ds_staging_enabled else 0
+    calls = {"fwd": lambda: lib.flexatt_fwd(p, T(q), T(k), T(v), T(o), lse.data_ptr(), sh)}
+    if ws_bytes:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        calls["delta"] = lambda: lib.flexatt_bwd_delta(p, T(o), T(do), delta.data_ptr(), sh)
+        calls["dkdv"] = lambda: lib.flexatt_bwd_dkdv_ds(p, T(q), T(k), T(v), T(do), lse.data_ptr(),
+                                                        delta.data_ptr(), T(dk), T(dv), ws.data_ptr(), ws_bytes, sh)
+        calls["dq"] = lambda: lib.flexatt_bwd_dq_ds(p, T(k), ws.data_ptr(), ws_bytes, T(dq), sh)
+    else:
+        calls["dq"] = lambda: lib.flexatt_bwd_dq_delta(p, T(q), T(k), T(v), T(o), T(do), lse.data_ptr(),
+                                                       delta.data_ptr(), T(dq), sh)
+        calls["dkdv"] = lambda: lib.flexatt_bwd_dkdv(p, T(q), T(k), T(v), T(do), lse.data_ptr(), delta.data_ptr(),
+                                                     T(dk), T(dv), sh)
     reps = max(args.steps, 10)
     kernel_ms = {}
     for name, fn in calls.items():
@@ -188,14 +200,16 @@ def main():
         kernel_ms[name] = statistics.median(a.elapsed_time(b) for a, b in evs)
 
     fwd_ms = kernel_ms["fwd"]
-    bwd_ms = kernel_ms["dq"] + kernel_ms["dkdv"]
+    bwd_ms = sum(v_ for k_, v_ in kernel_ms.items() if k_ != "fwd")
     fwd_tf = fwd_flop / fwd_ms / 1e9
     bwd_tf = bwd_flop / bwd_ms / 1e9
     total_tf = (fwd_flop + bwd_flop) / ms_step / 1e9
-    # dominant kernel = the longest one; its algorithmic FLOPs per launch:
-    # fwd: 4*D*pairs*B*Hq; dQ: 3 GEMMs of the 5 backward ones (S recompute,
-    # dP, dS K) = 6*D*pairs*B*Hq; dK/dV: 4 GEMMs (S, dP, P^T dO, dS^T Q) = 8*D*...
-    per_kernel_flop = {"fwd": fwd_flop, "dq": 6.0 * D * npairs * B * Hq, "dkdv": 8.0 * D * npairs * B * Hq}
+    # Roofline of the dominant (longest) kernel, with its share of the
+    # algorithmic FLOPs per launch: fwd 4*D*pairs*B*Hq; dK/dV 8*D*... (S, dP,
+    # P^T dO, dS^T Q: four of the five backward GEMMs); dQ 2*D*... (dS K).  The
+    # shares of the backward kernels add up to the 10*D convention; a dQ
+    # kernel that recomputes S and dP executes 6*D but is credited 2*D.
+    per_kernel_flop = {"fwd": fwd_flop, "dq": 2.0 * D * npairs * B * Hq, "dkdv": 8.0 * D * npairs * B * Hq}
     dom = max(per_kernel_flop, key=lambda n: kernel_ms[n])
     achieved = per_kernel_flop[dom] / kernel_ms[dom] / 1e9
 

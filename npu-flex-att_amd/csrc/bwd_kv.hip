@@ -81,7 +81,7 @@ struct KvCfg {
   static_assert(STAGEB % 256 == 0 && LDSB <= 160 * 1024, "LDS layout");
 };
 
-template <class T, int D, bool SOFTCAP, bool ALIBI>
+template <class T, int D, bool SOFTCAP, bool ALIBI, bool DS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void bwd_kv_kernel(BwdArgs a) {
   using C = KvCfg<D>;
@@ -369,6 +369,28 @@ void bwd_kv_kernel(BwdArgs a) {
       hi = lds_read_tr4(smem + (tb_hi[db] + off));
     };
     int s_tr = 0, s_cp = C::AHEAD % C::STAGES;  // stages of tiles u-1 and u+AHEAD
+    // Staged dS: tile u-1 (head ds_g, query tile ds_qt) leaves the exchange
+    // buffer transposed, lane = query row, as two 1 KB fragments of this
+    // pair's 32 KV rows (the dQ kernel's B operands).  Lane-constant part of
+    // the transpose-read address: this lane (group g = lane / 16) gathers
+    // query rows 4a .. 4a + 3, a = 4 (g & 1) + lane % 4, of KV row
+    // 4 (lane / 32) + (lane % 16) / 4 (+ 16 f + 8 half), from where the
+    // S-wave packed them (operand 2 + a / 4, lane (a & 1) * 32 + KV row,
+    // byte 8 ((a / 2) & 1)).
+    // dsp: this lane's 16 bytes of the unit of (head hk G + ds_g, query tile
+    // ds_qt, this KV block), moved per tile with the band counts of the query
+    // tiles it passes.
+    int ds_g = 0, ds_qt = qt_top;
+    int xtr = 0;
+    char* dsp = nullptr;
+    if constexpr (DS) {
+      const int aq = 4 * ((lane >> 4) & 1) + (lane & 3);
+      const int jr = 4 * (lane >> 5) + ((lane & 15) >> 2);
+      xtr = C::XOFF + pr * C::XB + (2 + (aq >> 2)) * 1024 + (((aq & 1) << 5) + jr) * 16 + 8 * ((aq >> 1) & 1);
+      const int64_t unit = (int64_t)(b * p.Hq + hk * p.G) * a.ds_head +
+                           ds_tile_offset(qt_top, p.causal, p.window, nkb) + kb - ds_kb_lo(qt_top, p.window, nkb);
+      dsp = a.ds + unit * kDsUnitB + (2 * pr) * 1024 + lane * 16;
+    }
 
     if (ntile > 0) {
 #pragma unroll
@@ -401,8 +423,37 @@ void bwd_kv_kernel(BwdArgs a) {
         PP[1] = *(const V8*)xslot(u - 1, 1);
         PS[0] = *(const V8*)xslot(u - 1, 2);
         PS[1] = *(const V8*)xslot(u - 1, 3);
+        i16x4 st4[4];
+        if constexpr (DS) {
+          const char* xb = smem + xtr + ((u - 1) & 1) * (C::NP * C::XB);
+#pragma unroll
+          for (int f = 0; f < 2; ++f) {
+            st4[2 * f] = lds_read_tr4(xb + (16 * f) * 16);
+            st4[2 * f + 1] = lds_read_tr4(xb + (16 * f + 8) * 16);
+          }
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) rdB(j, blo[j], bhi[j]);
+        if constexpr (DS) {
+          // streamed past the caches: each fragment is read once, by the dQ kernel
+#pragma unroll
+          for (int f = 0; f < 2; ++f)
+            __builtin_nontemporal_store(__builtin_bit_cast(i32x4, cat_tr<V8>(st4[2 * f], st4[2 * f + 1])),
+                                        (i32x4*)(dsp + f * 1024));
+          int64_t step;  // in units
+          if (++ds_g == p.G) {
+            // first head, query tile t = ds_qt - 1: the unit index moves by
+            // (offset(t) - kb_lo(t)) - (offset(t + 1) - kb_lo(t + 1)), and
+            // offset(t + 1) - offset(t) = kb_hi(t) - kb_lo(t)
+            const int t = ds_qt - 1;
+            step = ds_kb_lo(ds_qt, p.window, nkb) - ds_kb_hi(t, p.causal, nkb) - (int64_t)(p.G - 1) * a.ds_head;
+            ds_g = 0;
+            ds_qt = t;
+          } else {
+            step = a.ds_head;
+          }
+          dsp += step * kDsUnitB;
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();  // X(u)
@@ -423,7 +474,18 @@ void bwd_kv_kernel(BwdArgs a) {
       }
       if (ntile > 0) {
         advance();
-        wait_vmcnt<(C::AHEAD - 1) * CNT>();  // tile u+1 landed
+        // tile u+1 landed.  Stores count in vmcnt too: with staged dS, the
+        // two stores of each step s >= 1 from step u-3 on (2 min(u, 4) of
+        // them) were issued after tile u+1's copies and may stay in flight.
+        if constexpr (DS) {
+          if (u >= 4) wait_vmcnt<(C::AHEAD - 1) * CNT + 8>();
+          else if (u == 3) wait_vmcnt<(C::AHEAD - 1) * CNT + 6>();
+          else if (u == 2) wait_vmcnt<(C::AHEAD - 1) * CNT + 4>();
+          else if (u == 1) wait_vmcnt<(C::AHEAD - 1) * CNT + 2>();
+          else wait_vmcnt<(C::AHEAD - 1) * CNT>();
+        } else {
+          wait_vmcnt<(C::AHEAD - 1) * CNT>();
+        }
         s_cp = s_cp + 1 == C::STAGES ? 0 : s_cp + 1;
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -450,22 +512,25 @@ void bwd_kv_kernel(BwdArgs a) {
   }
 }
 
-template <class T, int D>
+template <class T, int D, bool DS>
 hipError_t launch_kv(const BwdArgs& a, hipStream_t st) {
   using C = KvCfg<D>;
+  static_assert(C::BKV == kDsKB && C::BM == kDsQT, "staged dS units are one tile by one KV block");
   BwdArgs x = a;
   x.ntiles = (a.p.Skv + C::BKV - 1) / C::BKV;
   const dim3 grid(x.ntiles * a.p.B * a.p.Hkv), block(C::NW * 64);
   const bool sc = a.p.cap > 0.f, al = a.p.alibi != nullptr;
-  if (sc && al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, true>), grid, block, 0, st, x);
-  else if (sc) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, false>), grid, block, 0, st, x);
-  else if (al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, true>), grid, block, 0, st, x);
-  else hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, false>), grid, block, 0, st, x);
+  if (sc && al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, true, DS>), grid, block, 0, st, x);
+  else if (sc) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, false, DS>), grid, block, 0, st, x);
+  else if (al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, true, DS>), grid, block, 0, st, x);
+  else hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, false, DS>), grid, block, 0, st, x);
   return hipGetLastError();
 }
 
-hipError_t bwd_kv_bf16_d128(const BwdArgs& a, hipStream_t st) { return launch_kv<__bf16, 128>(a, st); }
-hipError_t bwd_kv_f16_d128(const BwdArgs& a, hipStream_t st) { return launch_kv<_Float16, 128>(a, st); }
+hipError_t bwd_kv_bf16_d128(const BwdArgs& a, hipStream_t st) { return launch_kv<__bf16, 128, false>(a, st); }
+hipError_t bwd_kv_f16_d128(const BwdArgs& a, hipStream_t st) { return launch_kv<_Float16, 128, false>(a, st); }
+hipError_t bwd_kv_ds_bf16_d128(const BwdArgs& a, hipStream_t st) { return launch_kv<__bf16, 128, true>(a, st); }
+hipError_t bwd_kv_ds_f16_d128(const BwdArgs& a, hipStream_t st) { return launch_kv<_Float16, 128, true>(a, st); }
 
 #endif  // FLEXATT_D == 128
 

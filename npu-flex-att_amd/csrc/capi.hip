@@ -265,6 +265,32 @@ int bwd_common(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_
   a.ntiles = 0;
   a.o = View{nullptr, 0, 0, 0};
   a.delta_out = nullptr;
+  a.ds = nullptr;
+  a.ds_head = 0;
+  return FLEXATT_OK;
+}
+
+// Staged dS (D = 128 fp16/bf16, no document mask): units per query head and
+// workspace bytes; 0 when the problem takes the recomputing dQ kernel.
+bool ds_applies(const flexatt_problem* p) {
+  return (p->dtype == FLEXATT_F16 || p->dtype == FLEXATT_BF16) && p->head_dim == 128 && !p->doc_bounds;
+}
+int64_t ds_units_per_head(const flexatt_problem* p) {
+  const int nqt = (p->seqlen_q + kDsQT - 1) / kDsQT;
+  const int nkb = (p->seqlen_kv + kDsKB - 1) / kDsKB;
+  return ds_tile_offset(nqt, p->causal, p->sliding_window, nkb);
+}
+size_t ds_bytes(const flexatt_problem* p) {
+  if (!ds_applies(p)) return 0;
+  return (size_t)((int64_t)p->batch * p->heads_q * ds_units_per_head(p) * kDsUnitB);
+}
+int ds_workspace(const flexatt_problem* p, void* ws, size_t bytes, BwdArgs& a) {
+  if (!ds_applies(p)) return FLEXATT_ERANGE;
+  if (!ws) return FLEXATT_EINVAL;
+  if (bytes < ds_bytes(p)) return FLEXATT_EINVAL;
+  if (((uintptr_t)ws) % 16 != 0) return FLEXATT_ELAYOUT;
+  a.ds = (char*)ws;
+  a.ds_head = ds_units_per_head(p);
   return FLEXATT_OK;
 }
 
@@ -419,6 +445,58 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
   a.dk = mview(dk);
   a.dv = mview(dv);
   return (int)pick_dkdv(p)(a, (hipStream_t)stream);
+}
+
+size_t flexatt_bwd_workspace(const flexatt_problem* p) {
+  if (check_problem(p) != FLEXATT_OK) return 0;
+  return ds_bytes(p);
+}
+
+int flexatt_bwd_dkdv_ds(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                        const flexatt_tensor* v, const flexatt_tensor* dout, const float* lse, const float* delta,
+                        const flexatt_tensor* dk, const flexatt_tensor* dv, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  BwdArgs a;
+  FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
+  FLEXATT_TRY(check_out_tensor(dk, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
+  FLEXATT_TRY(check_out_tensor(dv, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
+  FLEXATT_TRY(ds_workspace(p, workspace, workspace_bytes, a));
+  a.dk = mview(dk);
+  a.dv = mview(dv);
+  return (int)(p->dtype == FLEXATT_BF16 ? bwd_kv_ds_bf16_d128 : bwd_kv_ds_f16_d128)(a, (hipStream_t)stream);
+}
+
+int flexatt_bwd_dq_ds(const flexatt_problem* p, const flexatt_tensor* k, const void* workspace,
+                      size_t workspace_bytes, const flexatt_tensor* dq, void* stream) {
+  FLEXATT_TRY(check_problem(p));
+  FLEXATT_TRY(check_tensor(k, p->dtype));
+  FLEXATT_TRY(check_out_tensor(dq, p->dtype, p->batch, p->heads_q, p->seqlen_q, p->head_dim));
+  BwdArgs a;
+  a.k = view(k);
+  a.dq = mview(dq);
+  a.p = make_shape(p);
+  a.ntiles = 0;
+  a.delta_out = nullptr;
+  FLEXATT_TRY(ds_workspace(p, (void*)workspace, workspace_bytes, a));
+  return (int)(p->dtype == FLEXATT_BF16 ? bwd_dq_ds_bf16_d128 : bwd_dq_ds_f16_d128)(a, (hipStream_t)stream);
+}
+
+int flexatt_bwd_ws(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                   const flexatt_tensor* v, const flexatt_tensor* o, const flexatt_tensor* dout, const float* lse,
+                   float* delta, const flexatt_tensor* dq, const flexatt_tensor* dk, const flexatt_tensor* dv,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  FLEXATT_TRY(check_problem(p));
+  if (!ds_applies(p)) return flexatt_bwd(p, q, k, v, o, dout, lse, delta, dq, dk, dv, stream);
+  BwdArgs a;
+  FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
+  FLEXATT_TRY(check_tensor(o, p->dtype));
+  FLEXATT_TRY(check_out_tensor(dq, p->dtype, p->batch, p->heads_q, p->seqlen_q, p->head_dim));
+  FLEXATT_TRY(check_out_tensor(dk, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
+  FLEXATT_TRY(check_out_tensor(dv, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
+  FLEXATT_TRY(ds_workspace(p, workspace, workspace_bytes, a));
+  FLEXATT_TRY(flexatt_bwd_delta(p, o, dout, delta, stream));
+  FLEXATT_TRY(flexatt_bwd_dkdv_ds(p, q, k, v, dout, lse, delta, dk, dv, workspace, workspace_bytes, stream));
+  return flexatt_bwd_dq_ds(p, k, workspace, workspace_bytes, dq, stream);
 }
 
 }  // extern "C"

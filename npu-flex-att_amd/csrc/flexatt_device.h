@@ -129,6 +129,21 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// 16 bytes global -> registers, issued through asm like load_lds16 so that
+// the compiler's wait counting does not see it; the data may be read only
+// after wait_vmcnt_tied<N>(...) names the destination registers (the tie
+// keeps every use of them after the wait).
+__device__ __forceinline__ void load16_async(i32x4& dst, const void* gptr) {
+  asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(dst) : "v"(gptr) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_tied(i32x4& a, i32x4& b, i32x4& c, i32x4& d, i32x4& e, i32x4& f,
+                                                i32x4& g, i32x4& h) {
+  asm volatile("s_waitcnt vmcnt(%8)"
+               : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f), "+v"(g), "+v"(h)
+               : "n"(N)
+               : "memory");
+}
 __device__ __forceinline__ unsigned lds_addr_of(const void* p) {
   return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
@@ -312,6 +327,53 @@ __device__ __forceinline__ void doc_bounds(const Shape& p, int b, int s, int& lo
     lo = 0;
     hi = 0x7fffffff;
   }
+}
+
+// --- staged dS (the D = 128 backward) -----------------------------------------
+// The dK/dV kernel writes the dS it feeds its own MFMAs (rounded to the input
+// dtype, without the softmax scale) to a workspace, and the dQ kernel forms
+// dQ = scale * dS K from it without recomputing S and dP.  The unit is one
+// (query tile of 32 rows, KV block of 128 rows) pair of one query head:
+// 8 fragments of 1 KB, fragment f holding KV rows 16 f .. 16 f + 15 as the
+// B operand of a 32x32x16 MFMA: lane l, element e is query row l % 32 and KV
+// row 16 f + 4 (l / 32) + e (e < 4), 16 f + 8 + 4 (l / 32) + e - 4 (e >= 4)
+// (the k order of the K^T transpose reads).  Only the pairs inside the
+// causal / window band are stored: query tile t holds KV blocks
+// [ds_kb_lo(t), ds_kb_hi(t)), the tiles of one head follow each other in t
+// order, and the heads in (b, h) order.
+constexpr int kDsQT = 32;     // query rows per dS unit
+constexpr int kDsKB = 128;    // KV rows per dS unit
+constexpr int kDsUnitB = 8192;  // bytes per dS unit (16-bit elements)
+
+__host__ __device__ __forceinline__ int ds_kb_lo(int t, int window, int nkb) {
+  if (window <= 0) return 0;
+  const int x = kDsQT * t - window;  // first key row any row of the tile keeps
+  const int lo = x > 0 ? x / kDsKB : 0;
+  return lo < nkb ? lo : nkb;
+}
+__host__ __device__ __forceinline__ int ds_kb_hi(int t, int causal, int nkb) {
+  if (!causal) return nkb;
+  const int hi = t / (kDsKB / kDsQT) + 1;  // last key row of the tile is 32 t + 31
+  return hi < nkb ? hi : nkb;
+}
+// sum over u in [0, x) of min(n, floor(u / 4)) (0 for x <= 0)
+__host__ __device__ __forceinline__ int64_t ds_quarter_sum(int64_t x, int64_t n) {
+  if (x <= 0) return 0;
+  if (x <= 4 * n) {
+    const int64_t q = x >> 2, r = x & 3;
+    return 2 * q * (q - 1) + r * q;
+  }
+  return 2 * n * (n - 1) + (x - 4 * n) * n;
+}
+// Units stored for query tiles [0, t) of one head: the sum of
+// ds_kb_hi - ds_kb_lo, in closed form (kb_hi = min(nkb, t/4 + 1) and
+// kb_lo = min(nkb, max(0, floor((t - ceil(W/32)) / 4))) are clamped quarter
+// steps).
+__host__ __device__ __forceinline__ int64_t ds_tile_offset(int t, int causal, int window, int nkb) {
+  static_assert(kDsKB == 4 * kDsQT, "closed form assumes four query tiles per KV block");
+  const int64_t hi = causal ? ds_quarter_sum((int64_t)t + 4, nkb) : (int64_t)t * nkb;
+  const int64_t lo = window > 0 ? ds_quarter_sum((int64_t)t - (window + kDsQT - 1) / kDsQT, nkb) : 0;
+  return hi - lo;
 }
 
 // allowed(i, j) for the masks of the path (j < Skv is the KV tail).

@@ -32,6 +32,11 @@ struct BwdArgs {
   // written for the dK/dV kernel; delta_out == nullptr: Delta is read from delta.
   View o;
   float* delta_out;
+  // Staged dS (D = 128 fp16/bf16): the workspace the dK/dV kernel writes and
+  // the dQ kernel reads, and the units stored per query head (the layout is
+  // described with ds_tile_offset); ds == nullptr: not staged.
+  char* ds;
+  int64_t ds_head;
 };
 
 // Split-KV decode forward (fwd_decode.hip): partials in the caller's workspace.
@@ -81,6 +86,13 @@ hipError_t fwd_decode_f16_d128(const DecodeArgs&, hipStream_t);
 // dK/dV as a KV-stationary tile stream (bwd_kv.hip), D = 128.
 hipError_t bwd_kv_bf16_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_f16_d128(const BwdArgs&, hipStream_t);
+
+// dK/dV that also writes its dS to a.ds (bwd_kv.hip), and dQ = scale * dS K
+// from it (bwd_dq_ds.hip), D = 128.
+hipError_t bwd_kv_ds_bf16_d128(const BwdArgs&, hipStream_t);
+hipError_t bwd_kv_ds_f16_d128(const BwdArgs&, hipStream_t);
+hipError_t bwd_dq_ds_bf16_d128(const BwdArgs&, hipStream_t);
+hipError_t bwd_dq_ds_f16_d128(const BwdArgs&, hipStream_t);
 
 // dQ as a query-stationary tile stream (bwd_q.hip), D = 128; with
 // a.delta_out set it also computes Delta (written there) from O and dO.

@@ -25,10 +25,14 @@ EXPORTS = (
     "flexatt_bwd_dq_delta",
     "flexatt_bwd_dkdv",
     "flexatt_bwd",
+    "flexatt_bwd_workspace",
+    "flexatt_bwd_ws",
+    "flexatt_bwd_dkdv_ds",
+    "flexatt_bwd_dq_ds",
     "flexatt_status_string",
     "flexatt_abi_version",
 )
-ABI_VERSION = 4
+ABI_VERSION = 5
 # Fixed scratch of flexatt_fwd_decode_noalloc (FLEXATT_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = 16 << 20
 
@@ -95,13 +99,17 @@ def load() -> ctypes.CDLL:
         "flexatt_bwd_dq_delta": [pr, T, T, T, T, T, fp, fp, T, st],
         "flexatt_bwd_dkdv": [pr, T, T, T, T, fp, fp, T, T, st],
         "flexatt_bwd": [pr, T, T, T, T, T, fp, fp, T, T, T, st],
+        "flexatt_bwd_ws": [pr, T, T, T, T, T, fp, fp, T, T, T, fp, ctypes.c_size_t, st],
+        "flexatt_bwd_dkdv_ds": [pr, T, T, T, T, fp, fp, T, T, fp, ctypes.c_size_t, st],
+        "flexatt_bwd_dq_ds": [pr, T, fp, ctypes.c_size_t, T, st],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = ctypes.c_int
-    lib.flexatt_fwd_decode_workspace.argtypes = [pr]
-    lib.flexatt_fwd_decode_workspace.restype = ctypes.c_size_t
+    for name in ("flexatt_fwd_decode_workspace", "flexatt_bwd_workspace"):
+        getattr(lib, name).argtypes = [pr]
+        getattr(lib, name).restype = ctypes.c_size_t
     lib.flexatt_status_string.argtypes = [ctypes.c_int]
     lib.flexatt_status_string.restype = ctypes.c_char_p
     lib.flexatt_abi_version.argtypes = []

@@ -45,6 +45,10 @@ _DTYPES = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _li
 # the problem is in their range: fp16/bf16, D <= 128 and (Hq / Hkv) * Sq <= 32.
 # Set to False to force the regular forward kernel (tests compare the two).
 decode_enabled = True
+# The backward stages dS through a workspace (flexatt_bwd_ws) whenever the
+# library supports it for the problem (fp16/bf16, head_dim 128, no document
+# mask).  Set to False to run the recomputing dQ kernel (flexatt_bwd).
+ds_staging_enabled = True
 _HEAD_DIMS = (32, 64, 128, 256)
 
 
@@ -267,7 +271,18 @@ def _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, *, causal,
     lse = lse.to(torch.float32).contiguous()
     slopes = _alibi(alibi, Hq, query.device)
     p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes, doc)
+    # head_dim 128 fp16/bf16: the dK/dV kernel stages its dS in a workspace
+    # from torch's caching allocator and dQ is formed from it
+    ws_bytes = lib.flexatt_bwd_workspace(p) if ds_staging_enabled else 0
     with torch.cuda.device(query.device):
+        if ws_bytes:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+            st = lib.flexatt_bwd_ws(p, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v), _lib.tensor(o),
+                                    _lib.tensor(do), lse.data_ptr(), delta.data_ptr(), _lib.tensor(DQ),
+                                    _lib.tensor(DK), _lib.tensor(DV), ws.data_ptr(), ws_bytes,
+                                    _stream(query.device))
+            _lib.check(st, "flexatt_bwd_ws")
+            return
         st = lib.flexatt_bwd(p, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v), _lib.tensor(o),
                              _lib.tensor(do), lse.data_ptr(), delta.data_ptr(), _lib.tensor(DQ),
                              _lib.tensor(DK), _lib.tensor(DV), _stream(query.device))

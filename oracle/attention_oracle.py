@@ -185,6 +185,35 @@ def delta(o: torch.Tensor, do: torch.Tensor, dtype: torch.dtype = torch.float64)
     return (o.detach().to("cpu", dtype) * do.detach().to("cpu", dtype)).sum(-1)
 
 
+def _score_grad(qf, kf, vf, dof, causal, sliding_window, alibi_slope, scale, soft_cap, o, dtype, document_ids):
+    """(dS / scale, P) [B, Hq, Sq, Skv] from prepared (expanded) inputs:
+    ``P (dP - Delta) (1 - tanh^2)``, 0 at masked pairs (npu_flash_attention.py
+    :386-397, :502-513)."""
+    sq = qf.shape[2]
+    x, t = scores(qf, kf, scale, soft_cap, alibi_slope)
+    ok = _mask(sq, x.shape[-1], causal, sliding_window, document_ids)
+    p, _ = _softmax_masked(x, ok)
+    of = torch.matmul(p, vf) if o is None else o.detach().to("cpu", dtype)
+    dl = (of * dof).sum(-1, keepdim=True)
+    dp = torch.matmul(dof, vf.transpose(-2, -1))
+    ds = p * (dp - dl)
+    if t is not None:
+        ds = ds * (1.0 - t * t)
+    return ds, p
+
+
+def score_grad(q, k, v, do, causal=False, sliding_window=0, alibi_slope=None, scale=None, soft_cap=0.0,
+               dtype=torch.float64, document_ids=None):
+    """Gradient of the loss with respect to the scaled, capped, biased logits
+    before the scale factor: ``dS / scale = P (dP - Delta) (1 - tanh^2)``,
+    [B, Hq, Sq, Skv], 0 at masked pairs.  :func:`backward` forms
+    ``dQ = scale dS K`` and ``dK = scale dS^T Q`` from exactly this tensor, so
+    it is pinned by backward's checks."""
+    qf, kf, vf, scale, _ = _prep(q, k, v, scale, dtype)
+    return _score_grad(qf, kf, vf, do.detach().to("cpu", dtype), causal, sliding_window, alibi_slope, scale,
+                       soft_cap, None, dtype, document_ids)[0]
+
+
 def backward(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -213,15 +242,8 @@ def backward(
     hkv = k.shape[1]
     qf, kf, vf, scale, g = _prep(q, k, v, scale, dtype)
     dof = do.detach().to("cpu", dtype)
-    x, t = scores(qf, kf, scale, soft_cap, alibi_slope)
-    ok = _mask(sq, x.shape[-1], causal, sliding_window, document_ids)
-    p, _ = _softmax_masked(x, ok)
-    of = torch.matmul(p, vf) if o is None else o.detach().to("cpu", dtype)
-    dl = (of * dof).sum(-1, keepdim=True)
-    dp = torch.matmul(dof, vf.transpose(-2, -1))
-    ds = p * (dp - dl)
-    if t is not None:
-        ds = ds * (1.0 - t * t)
+    ds, p = _score_grad(qf, kf, vf, dof, causal, sliding_window, alibi_slope, scale, soft_cap, o, dtype,
+                        document_ids)
     ds = ds * scale
     dq = torch.matmul(ds, kf)
     dk = torch.matmul(ds.transpose(-2, -1), qf)

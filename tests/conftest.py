@@ -22,3 +22,24 @@ def gpu_device():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     return torch.device("cuda:0")
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """Write the parity errors the GPU tests measured (gpu_helpers.RECORDS)
+    as JSON lines to $FLEXATT_PARITY_LOG, or gpurun_out/parity_errors.jsonl
+    when that folder exists."""
+    mod = sys.modules.get("gpu_helpers")
+    recs = getattr(mod, "RECORDS", None)
+    if not recs:
+        return
+    path = os.environ.get("FLEXATT_PARITY_LOG")
+    if not path:
+        out = os.path.join(ROOT, "gpurun_out")
+        if not os.path.isdir(out):
+            return
+        path = os.path.join(out, "parity_errors.jsonl")
+    import json
+
+    with open(path, "w") as f:
+        for r in recs:
+            f.write(json.dumps(r) + "\n")

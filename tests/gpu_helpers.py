@@ -8,22 +8,27 @@ Tolerance criterion (stated once, used everywhere):
     err(x, ref) = max|x - ref| / max(1, max|ref|)
 i.e. max-abs error for O(1) tensors and max-abs relative to the tensor's
 magnitude for large gradients.  The oracle runs in float64 on the same
-(rounded) inputs.
+(rounded) inputs.  Every checked error, with the plain max-abs error beside
+it, is recorded in RECORDS; the test session writes them to a JSON-lines file
+(see conftest.py) so a GPU run returns the measured numbers.
 """
 import math
+import os
 
 import torch
 
 from oracle import attention_oracle as orc
 
-# north-star tolerances (max-abs 5e-3 fp16, 2e-2 bf16 relative to fp32) for
-# the forward; the gradients carry the extra rounding of P and dS to the input
-# dtype before their MFMAs (as in the reference kernels) and get 2x.
+# north-star tolerances (max-abs 5e-3 fp16, 2e-2 bf16 relative to the fp32 /
+# float64 eager math) for all five outputs; LSE is held tighter.
 TOL = {
     torch.float32: {"o": 1e-5, "lse": 1e-5, "dq": 1e-4, "dk": 1e-4, "dv": 1e-4},
-    torch.float16: {"o": 5e-3, "lse": 1e-3, "dq": 1e-2, "dk": 1e-2, "dv": 1e-2},
-    torch.bfloat16: {"o": 2e-2, "lse": 5e-3, "dq": 4e-2, "dk": 4e-2, "dv": 4e-2},
+    torch.float16: {"o": 5e-3, "lse": 1e-3, "dq": 5e-3, "dk": 5e-3, "dv": 5e-3},
+    torch.bfloat16: {"o": 2e-2, "lse": 5e-3, "dq": 2e-2, "dk": 2e-2, "dv": 2e-2},
 }
+
+# One dict per checked output: test id, output name, dtype, err, max-abs, tol.
+RECORDS = []
 
 
 def draw(seed, b, hq, hkv, sq, skv, d, dtype, scale_inputs=1.0, device="cuda"):
@@ -36,22 +41,29 @@ def draw(seed, b, hq, hkv, sq, skv, d, dtype, scale_inputs=1.0, device="cuda"):
     return cpu, [t.to(device) for t in cpu]
 
 
-def err(x, ref):
+def err_abs(x, ref):
+    """(err, plain max-abs error) over the entries where ref is finite."""
     x = x.detach().to("cpu", torch.float64)
     ref = ref.detach().to("cpu", torch.float64)
     fin = torch.isfinite(ref)
     assert torch.equal(torch.isfinite(x), fin), "non-finite pattern differs"
     if not bool(fin.any()):
-        return 0.0
+        return 0.0, 0.0
     d = (x[fin] - ref[fin]).abs().max().item()
-    return d / max(1.0, ref[fin].abs().max().item())
+    return d / max(1.0, ref[fin].abs().max().item()), d
+
+
+def err(x, ref):
+    return err_abs(x, ref)[0]
 
 
 def check(name, x, ref, dtype, report=None, factor=1.0):
-    e = err(x, ref)
+    e, d = err_abs(x, ref)
     tol = TOL[dtype][name] * factor
     if report is not None:
         report[name] = e
+    RECORDS.append({"test": os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0], "out": name,
+                    "dtype": str(dtype).replace("torch.", ""), "err": e, "max_abs": d, "tol": tol})
     assert e <= tol, f"{name}: err {e:.3e} > tol {tol:.1e}"
     return e
 

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_status_strings():
     lib = L.load()
     assert lib.flexatt_abi_version() == L.ABI_VERSION
-    assert b"#define FLEXATT_ABI_VERSION 4" in open(HEADER, "rb").read()
+    assert f"#define FLEXATT_ABI_VERSION {L.ABI_VERSION}".encode() in open(HEADER, "rb").read()
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.flexatt_status_string(code)
     assert b"head_dim" in lib.flexatt_status_string(-3)
@@ -215,3 +215,79 @@ def test_header_struct_layout_compiled(tmp_path):
     want = [getattr(L.Problem, f[0]).offset for f in L.Problem._fields_] + \
            [getattr(L.Tensor, f[0]).offset for f in L.Tensor._fields_]
     assert vals[2:] == want
+
+
+def _staged_units(sq, skv, causal, window):
+    """Units (32-row query tile t, 128-row KV block kb) the dK/dV kernel
+    visits, per its rule: block kb covers query rows [q_lo, q_hi) with
+    q_lo = 128 kb if causal else 0 and q_hi = min(Sq, 128 kb + 128 + W) with
+    a window; also check that every unit holding an attended pair is among
+    them."""
+    nkb = -(-skv // 128)
+    units = set()
+    for kb in range(nkb):
+        q_lo = 128 * kb if causal else 0
+        q_hi = min(sq, 128 * kb + 128 + window) if window > 0 else sq
+        if q_hi > q_lo:
+            for t in range(q_lo // 32, -(-q_hi // 32)):
+                units.add((t, kb))
+    for t in range(-(-sq // 32)):
+        for kb in range(nkb):
+            j0, j1 = 128 * kb, min(skv, 128 * kb + 128) - 1
+            # some row i of the tile keeps a key j of the block: j <= i (causal), i - j <= W (window)
+            hit = any(max(j0, i - window if window else j0) <= (min(j1, i) if causal else j1)
+                      for i in range(32 * t, min(sq, 32 * t + 32)))
+            if hit:
+                assert (t, kb) in units, (sq, skv, causal, window, t, kb)
+    # the band each query tile is given in the workspace (ds_kb_lo / ds_kb_hi
+    # of flexatt_device.h) is exactly the visited set, so every store lands
+    # in its own slot
+    band = set()
+    for t in range(-(-sq // 32)):
+        lo = min(nkb, max(0, (32 * t - window) // 128)) if window > 0 else 0
+        hi = min(nkb, t // 4 + 1) if causal else nkb
+        band.update((t, kb) for kb in range(lo, hi))
+    assert band == units
+    return len(units)
+
+
+@pytest.mark.parametrize("sq,skv", [(1, 1), (31, 33), (128, 128), (300, 129), (4096, 4096), (1000, 257),
+                                    (129, 1000), (16384, 16383), (777, 5000)])
+@pytest.mark.parametrize("causal,window", [(0, 0), (1, 0), (1, 1), (1, 100), (0, 33), (1, 128), (1, 2048), (0, 4096)])
+def test_bwd_workspace_counts_the_band(sq, skv, causal, window):
+    """flexatt_bwd_workspace (closed form of the staged-dS band) equals the
+    units the dK/dV kernel visits, times B * Hq * 8 KB; 0 off its range."""
+    lib = L.load()
+    p = problem(batch=2, heads_q=6, heads_kv=2, seqlen_q=sq, seqlen_kv=skv, head_dim=128, causal=causal,
+                sliding_window=window)
+    assert lib.flexatt_bwd_workspace(p) == 2 * 6 * _staged_units(sq, skv, causal, window) * 8192
+
+
+def test_bwd_workspace_range():
+    lib = L.load()
+    ws = lib.flexatt_bwd_workspace
+    assert ws(problem(head_dim=128)) > 0
+    assert ws(problem(head_dim=128, dtype=L.F16)) > 0
+    assert ws(problem(head_dim=64)) == 0
+    assert ws(problem(head_dim=256)) == 0
+    assert ws(problem(head_dim=128, dtype=L.F32)) == 0
+    assert ws(problem(head_dim=128, doc_bounds=FAKE)) == 0
+    assert ws(problem(head_dim=128, heads_q=3)) == 0  # invalid problem
+
+
+def test_staged_bwd_rejections():
+    lib = L.load()
+    t = tens(stride_b=4 * 64 * 128, stride_h=64 * 128, stride_s=128)
+    p = problem(head_dim=128)
+    need = lib.flexatt_bwd_workspace(p)
+    st = lib.flexatt_bwd_dkdv_ds(p, t, t, t, t, FAKE, FAKE, t, t, FAKE, need - 1, None)
+    assert st == -1
+    assert lib.flexatt_bwd_dkdv_ds(p, t, t, t, t, FAKE, FAKE, t, t, None, need, None) == -1
+    assert lib.flexatt_bwd_dkdv_ds(p, t, t, t, t, FAKE, FAKE, t, t, FAKE + 8, need, None) == -5
+    assert lib.flexatt_bwd_dq_ds(p, t, FAKE, need - 1, t, None) == -1
+    assert lib.flexatt_bwd_dq_ds(problem(head_dim=64), tens(), FAKE, need, tens(), None) == -6
+    assert lib.flexatt_bwd_dkdv_ds(problem(head_dim=64), tens(), tens(), tens(), tens(), FAKE, FAKE, tens(),
+                                   tens(), FAKE, need, None) == -6
+    assert lib.flexatt_bwd_ws(p, t, t, t, t, t, FAKE, FAKE, t, t, t, FAKE, need - 1, None) == -1
+    assert lib.flexatt_bwd_ws(p, t, t, t, t, t, FAKE, FAKE, tens(stride_h=0, stride_s=128), t, t, FAKE, need,
+                              None) == -5
