@@ -38,6 +38,10 @@ CONFIGS = {
     "gqa_llama3_8b": (2, 32, 8, 4096, 4096, 128, "bf16", True, 0, 0.0, False, None, 1.0),
     "gemma2_d256": (1, 16, 8, 8192, 8192, 256, "bf16", True, 4096, 50.0, False, 1.0 / 16, 2.0),
     "all_primitives_d64": (1, 28, 4, 16384, 16383, 64, "fp16", True, 2048, 30.0, True, 0.05, 1.0),
+    # the reference's own perf-table shapes (RESULT.md:163-167)
+    "mha_d64_s128": (1, 2, 2, 128, 128, 64, "fp16", True, 0, 0.0, False, None, 1.0),
+    "mha_d64_s512": (1, 2, 2, 512, 512, 64, "fp16", True, 0, 0.0, False, None, 1.0),
+    "mha_d64_s1024": (1, 2, 2, 1024, 1024, 64, "fp16", True, 0, 0.0, False, None, 1.0),
     "mha_d64_s2048": (1, 2, 2, 2048, 2048, 64, "fp16", True, 0, 0.0, False, None, 1.0),
 }
 # Decoding workloads (forward only, split-KV kernels): one new token per
