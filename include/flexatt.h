@@ -75,12 +75,28 @@ typedef struct flexatt_problem {
   int32_t sliding_window; /* W > 0: keep i - j <= W; 0: off */
   float soft_cap;         /* c > 0: x -> c * tanh(x / c); 0: off */
   const float* alibi_slopes; /* device fp32 [Hq]: x += slope[h] * (i - j); NULL: off */
-  /* Document mask (no counterpart in the reference, which lists document
-   * masking as future work, README.md:219): device int32 [B, S, 2] holding,
-   * for position s of batch b, the range [lo, hi) of positions of its
-   * document; i and j attend to each other only inside one document, on top
-   * of the other primitives.  Needs seqlen_q == seqlen_kv = S.  NULL: off. */
+  /* Interval masks (no counterpart in the reference, which lists document
+   * masking and PrefixLM as future work, README.md:219, DESIGN.md:374):
+   * device int32 [B, Sq, 2] holding, for query row i of batch b, the range
+   * [lo, hi) of keys it may attend, on top of the other primitives.  Both
+   * bounds must be non-decreasing in i.  A document mask is symmetric: the
+   * range of positions of i's document (then col_bounds may stay NULL and
+   * seqlen_q == seqlen_kv).  NULL: off. */
   const int32_t* doc_bounds;
+  /* The transpose of doc_bounds for a mask that is not symmetric (PrefixLM):
+   * device int32 [B, Skv, 2], for key j the range [lo, hi) of query rows
+   * that may attend it, both non-decreasing in j; it must describe the same
+   * mask as doc_bounds.  NULL: doc_bounds is symmetric and read as both. */
+  const int32_t* col_bounds;
+  /* Block-sparse mask (the reference lists the block-sparse BlockMask index
+   * format as unsupported, README.md:198): device uint8 [B, block_heads,
+   * ceil(Sq / 128), ceil(Skv / 128)]; a zero entry removes the 128 x 128
+   * block of (query rows, keys) from the attention of those heads, on top of
+   * the other primitives.  block_heads is 1 (one map for every head) or
+   * heads_q; ceil(Skv / 128) <= 2048.  NULL: off. */
+  const uint8_t* block_map;
+  int32_t block_heads;
+  int32_t reserved; /* 0 */
 } flexatt_problem;
 
 /* Forward: o = softmax(mask(score(q k^T))) v and lse.
@@ -135,8 +151,8 @@ int flexatt_bwd_dq(const flexatt_problem* p, const flexatt_tensor* q, const flex
                    const float* delta, const flexatt_tensor* dq, void* stream);
 
 /* Backward Delta and dQ in one pass where the dQ kernel can form Delta itself
- * (fp16/bf16, head_dim 128, no document mask; otherwise the Delta pass then
- * dQ): delta (the caller's fp32 [B,Hq,Sq] buffer) receives sum_d o * dout,
+ * (fp16/bf16, head_dim 128, no interval or block mask; otherwise the Delta
+ * pass then dQ): delta (the caller's fp32 [B,Hq,Sq] buffer) receives sum_d o * dout,
  * for flexatt_bwd_dkdv after it.  Replaces the Delta op and the
  * flash_attn_bwd_dq_kernel launch of npu_flash_attention_backward,
  * npu_flash_attention.py:681-712. */
@@ -160,13 +176,13 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
                 const float* lse, float* delta, const flexatt_tensor* dq, const flexatt_tensor* dk,
                 const flexatt_tensor* dv, void* stream);
 
-/* Backward with dS staged through HBM (fp16/bf16, head_dim 128, no
- * document mask).  The dK/dV kernel already forms dS for every attended
+/* Backward with dS staged through HBM (fp16/bf16, head_dim 128).  The dK/dV kernel already forms dS for every attended
  * pair; it writes those values (rounded to the input dtype, as its own dK
  * MFMAs consume them) to a caller-owned workspace, and the dQ kernel forms
  * dQ = scale * dS K from them instead of recomputing S and dP.  The
  * workspace holds 2 bytes per attended (query row, KV row) pair of each
- * query head, in 32 x 128 units over the causal / window band:
+ * query head, in 32 x 128 units over the causal / window band (interval
+ * and block masks keep that band; their masked pairs hold zeros):
  * flexatt_bwd_workspace(p) bytes (0: the problem is outside this range),
  * 16-byte aligned, not zeroed, reusable once the call's work on `stream` is
  * done.  Same results as flexatt_bwd up to fp32 summation order; bitwise
@@ -202,7 +218,7 @@ const char* flexatt_status_string(int status);
 /* ABI version of this header (bumped on any signature change). */
 int flexatt_abi_version(void);
 
-#define FLEXATT_ABI_VERSION 5
+#define FLEXATT_ABI_VERSION 6
 
 #ifdef __cplusplus
 }

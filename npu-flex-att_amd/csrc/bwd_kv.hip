@@ -159,6 +159,19 @@ void bwd_kv_kernel(BwdArgs a) {
     constexpr bool RAW = !SOFTCAP && !ALIBI;
     const float c2 = p.scale_log2;
     const bool kv_tail = kw0 + 32 > p.Skv;
+    // Interval masks (document masks, PrefixLM): the query rows [clo, chi)
+    // that may attend this lane's KV row; a tile needs no per-element test
+    // when it lies inside [clo of the pair's last KV row, chi of its first)
+    // (the bounds are non-decreasing).
+    int clo, chi, pc_lo = 0, pc_hi = 0x7fffffff;
+    col_bounds(p, b, min(my_kv, p.Skv - 1), clo, chi);
+    if (p.docc) {
+      int l0, h0, l1, h1;
+      col_bounds(p, b, min(kw0, p.Skv - 1), l0, h0);
+      col_bounds(p, b, min(kw0 + 31, p.Skv - 1), l1, h1);
+      pc_lo = l1;
+      pc_hi = h0;
+    }
     int cg = 0, cqt = qt_top;  // tile being formed (head, query tile)
     int sc = 0;               // its stage
 
@@ -167,6 +180,12 @@ void bwd_kv_kernel(BwdArgs a) {
       const bool act = u < ntile;
       f32x16 S, DP;        // Q K^T and Delta - dO V^T (the latter accumulated from Delta)
       f32x4 L4[4];         // LSE (to log2 units) of this lane's query rows
+      // block-sparse mask: whether tile u's 128 x 128 block is computed (read
+      // here, used in V(u); the S-wave has no other memory operation in flight)
+      bool live = true;
+      if (p.blk && act)
+        live = __builtin_amdgcn_readfirstlane(block_on(p, b, hk * p.G + cg, min(cqt * C::BM, p.Sq - 1),
+                                                       min(kw0, p.Skv - 1)));
       // ---- M(u): S = Q K^T, DP = Delta - dO V^T of tile u; LSE reads ------
       if (act) {
         // Row-read addresses of this stage (the Q / dO choice folds into the
@@ -244,7 +263,7 @@ void bwd_kv_kernel(BwdArgs a) {
             if constexpr (decltype(masked)::value) {
               const int q = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
               const bool ok = (q < p.Sq) & (my_kv < p.Skv) & (!p.causal | (my_kv <= q)) &
-                              ((p.window == 0) | (q - my_kv <= p.window));
+                              ((p.window == 0) | (q - my_kv <= p.window)) & (q >= clo) & (q < chi) & live;
               e = ok ? e : 0.f;
             }
             pe[r] = e;
@@ -263,7 +282,7 @@ void bwd_kv_kernel(BwdArgs a) {
           *(V8*)xslot(u, 3) = pack8<T>(de, 8);
         };
         if ((m0 + C::BM > p.Sq) || kv_tail || (p.causal && m0 < kw0 + 31) ||
-            (p.window > 0 && m0 + C::BM - 1 - kw0 > p.window))
+            (p.window > 0 && m0 + C::BM - 1 - kw0 > p.window) || m0 < pc_lo || m0 + C::BM > pc_hi || !live)
           form(std::true_type{});
         else
           form(std::false_type{});

@@ -167,7 +167,8 @@ void bwd_dq_mfma_kernel(BwdArgs a) {
 
     const int n0 = t * C::BN;
     const bool skip = (p.causal && n0 > mw + 31) || (p.window > 0 && mw - (n0 + C::BN - 1) > p.window) ||
-                      n0 >= whi || n0 + C::BN <= wlo;
+                      n0 >= whi || n0 + C::BN <= wlo ||
+                      !__builtin_amdgcn_readfirstlane(block_on(p, b, hq, min(mw, p.Sq - 1), n0));
     if (skip) continue;
     const bool full = (n0 + C::BN <= p.Skv) && (!p.causal || n0 + C::BN - 1 <= mw) &&
                       (p.window == 0 || mw + 31 - n0 <= p.window) && !p.doc;
@@ -273,18 +274,18 @@ void bwd_dkdv_mfma_kernel(BwdArgs a) {
   int q_lo = p.causal ? n0 : 0;
   int q_hi = p.Sq;
   if (p.window > 0) q_hi = min(q_hi, n0 + C::BNK + p.window);
-  // document masks (symmetric): the query range of this lane's KV row, of
-  // the workgroup's and of this wave's KV rows
+  // interval masks: the query range of this lane's KV row (column bounds),
+  // of the workgroup's and of this wave's KV rows
   int dlo, dhi, wlo = 0, whi = 0x7fffffff;
-  doc_bounds(p, b, min(my_n, p.Skv - 1), dlo, dhi);
-  if (p.doc) {
+  col_bounds(p, b, min(my_n, p.Skv - 1), dlo, dhi);
+  if (p.docc) {
     int l0, h0, l1, h1;
-    doc_bounds(p, b, min(n0, p.Skv - 1), l0, h0);
-    doc_bounds(p, b, min(n0 + C::BNK, p.Skv) - 1, l1, h1);
+    col_bounds(p, b, min(n0, p.Skv - 1), l0, h0);
+    col_bounds(p, b, min(n0 + C::BNK, p.Skv) - 1, l1, h1);
     q_lo = max(q_lo, l0);
     q_hi = min(q_hi, h1);
-    doc_bounds(p, b, min(nw, p.Skv - 1), wlo, h0);
-    doc_bounds(p, b, min(nw + 31, p.Skv - 1), l1, whi);
+    col_bounds(p, b, min(nw, p.Skv - 1), wlo, h0);
+    col_bounds(p, b, min(nw + 31, p.Skv - 1), l1, whi);
   }
   const int qt_lo = q_lo / C::BMQ;
   const int qt_hi = (q_hi + C::BMQ - 1) / C::BMQ;
@@ -356,7 +357,8 @@ void bwd_dkdv_mfma_kernel(BwdArgs a) {
       const int hq = hk * p.G + g;
       const int mt = (qt_lo + it % nq) * C::BMQ;
       const bool skip = (p.causal && mt + C::BMQ - 1 < nw) || (p.window > 0 && mt - (nw + 31) > p.window) ||
-                        mt >= whi || mt + C::BMQ <= wlo;
+                        mt >= whi || mt + C::BMQ <= wlo ||
+                        !__builtin_amdgcn_readfirstlane(block_on(p, b, hq, min(mt, p.Sq - 1), min(nw, p.Skv - 1)));
       if (skip) continue;
       const bool full = (!p.causal || mt >= nw + 31) && (p.window == 0 || mt + C::BMQ - 1 - nw <= p.window) &&
                         !p.doc;

@@ -36,7 +36,13 @@ int check_problem(const flexatt_problem* p) {
   if (p->batch <= 0 || p->heads_q <= 0 || p->heads_kv <= 0 || p->seqlen_q <= 0 || p->seqlen_kv <= 0)
     return FLEXATT_EINVAL;
   if (p->heads_q % p->heads_kv != 0) return FLEXATT_ESHAPE;
-  if (p->doc_bounds && p->seqlen_q != p->seqlen_kv) return FLEXATT_ESHAPE;
+  if (p->doc_bounds && !p->col_bounds && p->seqlen_q != p->seqlen_kv) return FLEXATT_ESHAPE;
+  if (p->col_bounds && !p->doc_bounds) return FLEXATT_EINVAL;
+  if (p->reserved != 0) return FLEXATT_EINVAL;
+  if (p->block_map) {
+    if (p->block_heads != 1 && p->block_heads != p->heads_q) return FLEXATT_EINVAL;
+    if ((p->seqlen_kv + kBlk - 1) / kBlk > kBlkRowMax) return FLEXATT_ERANGE;
+  }
   if (head_index(p->head_dim) < 0) return FLEXATT_EHEADDIM;
   if (p->causal != 0 && p->causal != 1) return FLEXATT_EINVAL;
   if (p->sliding_window < 0) return FLEXATT_EINVAL;
@@ -109,6 +115,11 @@ Shape make_shape(const flexatt_problem* p) {
   s.cap_log2 = p->soft_cap * kLog2e;
   s.alibi = p->alibi_slopes;
   s.doc = p->doc_bounds;
+  s.docc = p->col_bounds ? p->col_bounds : p->doc_bounds;
+  s.blk = p->block_map;
+  s.blk_h = p->block_map ? p->block_heads : 1;
+  s.blk_nq = (p->seqlen_q + kBlk - 1) / kBlk;
+  s.blk_nk = (p->seqlen_kv + kBlk - 1) / kBlk;
   return s;
 }
 
@@ -137,6 +148,7 @@ constexpr int kDecWaves = 4;  // waves per workgroup
 constexpr int kDecTile = 32;   // KV rows per tile
 bool decode_applies(const flexatt_problem* p) {
   return (p->dtype == FLEXATT_F16 || p->dtype == FLEXATT_BF16) && p->head_dim <= 128 && !p->doc_bounds &&
+         !p->block_map &&
          (int64_t)(p->heads_q / p->heads_kv) * p->seqlen_q <= 32;
 }
 struct DecodePlan {
@@ -223,10 +235,11 @@ int scratch_for_stream(hipStream_t stream, void** out) {
   return FLEXATT_OK;
 }
 
-// Document masks run on the general backward kernels (the D = 128 tile
-// streams have no document bounds).
+// Interval and block masks take the general dQ kernel (the recomputing
+// D = 128 tile stream has neither); the D = 128 dK/dV tile stream has both.
+bool has_masks(const flexatt_problem* p) { return p->doc_bounds || p->block_map; }
 BwdLauncher pick_dq(const flexatt_problem* p) {
-  if (p->doc_bounds && p->head_dim == 128 && p->dtype != FLEXATT_F32)
+  if (has_masks(p) && p->head_dim == 128 && p->dtype != FLEXATT_F32)
     return p->dtype == FLEXATT_BF16 ? bwd_dq_mfma_bf16_d128 : bwd_dq_mfma_f16_d128;
   return kDq[p->dtype][head_index(p->head_dim)];
 }
@@ -234,11 +247,7 @@ BwdLauncher pick_dq(const flexatt_problem* p) {
 bool dq_fuses_delta(const flexatt_problem* p) {
   return pick_dq(p) == (p->dtype == FLEXATT_BF16 ? bwd_q_bf16_d128 : bwd_q_f16_d128);
 }
-BwdLauncher pick_dkdv(const flexatt_problem* p) {
-  if (p->doc_bounds && p->head_dim == 128 && p->dtype != FLEXATT_F32)
-    return p->dtype == FLEXATT_BF16 ? bwd_dkdv_mfma_bf16_d128 : bwd_dkdv_mfma_f16_d128;
-  return kDkdv[p->dtype][head_index(p->head_dim)];
-}
+BwdLauncher pick_dkdv(const flexatt_problem* p) { return kDkdv[p->dtype][head_index(p->head_dim)]; }
 
 #define FLEXATT_TRY(x)             \
   do {                             \
@@ -270,10 +279,12 @@ int bwd_common(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_
   return FLEXATT_OK;
 }
 
-// Staged dS (D = 128 fp16/bf16, no document mask): units per query head and
-// workspace bytes; 0 when the problem takes the recomputing dQ kernel.
+// Staged dS (D = 128 fp16/bf16, every mask primitive: the dK/dV kernel
+// masks per element and stores every unit of the causal / window band, zero
+// where masked): units per query head and workspace bytes; 0 when the
+// problem takes the recomputing dQ kernel.
 bool ds_applies(const flexatt_problem* p) {
-  return (p->dtype == FLEXATT_F16 || p->dtype == FLEXATT_BF16) && p->head_dim == 128 && !p->doc_bounds;
+  return (p->dtype == FLEXATT_F16 || p->dtype == FLEXATT_BF16) && p->head_dim == 128;
 }
 int64_t ds_units_per_head(const flexatt_problem* p) {
   const int nqt = (p->seqlen_q + kDsQT - 1) / kDsQT;

@@ -59,7 +59,11 @@ struct Shape {
   float tanh_k;       // 2 log2(e) scale / cap: exp2(s * tanh_k) = e^(2 scale s / cap)
   float cap_log2;     // cap * log2(e)
   const float* alibi;  // [Hq] or nullptr
-  const int* doc;      // [B][S][2] document bounds (Sq == Skv = S) or nullptr
+  const int* doc;      // row bounds [B][Sq][2]: keys [lo, hi) query row i may attend, or nullptr
+  const int* docc;     // column bounds [B][Skv][2]: query rows [lo, hi) that may attend key j
+                       // (the same array as doc for a symmetric mask), or nullptr
+  const unsigned char* blk;  // block map [B][blk_h][blk_nq][blk_nk] of 128 x 128 blocks, or nullptr
+  int blk_h, blk_nq, blk_nk;
 };
 
 // --- element traits ----------------------------------------------------------
@@ -314,19 +318,41 @@ __device__ __forceinline__ float score_log2(float s, const Shape& p, float slope
   return score_log2_d<SOFTCAP, ALIBI>(s, p, slope_log2, (float)(i - j), t);
 }
 
-// Document bounds [lo, hi) of position s of batch b: the other positions of
-// its document; [0, INT_MAX) when document masking is off.  Bounds are
-// non-decreasing in s, so those of a range's first and last positions bound
-// the whole range.
-__device__ __forceinline__ void doc_bounds(const Shape& p, int b, int s, int& lo, int& hi) {
+// Interval masks (document masks, PrefixLM): the keys [lo, hi) query row i
+// of batch b may attend; [0, INT_MAX) when off.  Both bounds are
+// non-decreasing in i, so those of a range's first and last rows bound the
+// whole range.
+__device__ __forceinline__ void doc_bounds(const Shape& p, int b, int i, int& lo, int& hi) {
   if (p.doc) {
-    const int* d = p.doc + ((int64_t)b * p.Skv + s) * 2;
+    const int* d = p.doc + ((int64_t)b * p.Sq + i) * 2;
     lo = d[0];
     hi = d[1];
   } else {
     lo = 0;
     hi = 0x7fffffff;
   }
+}
+// The transpose: the query rows [lo, hi) that may attend key j (for the
+// KV-stationary kernels); non-decreasing in j as well.
+__device__ __forceinline__ void col_bounds(const Shape& p, int b, int j, int& lo, int& hi) {
+  if (p.docc) {
+    const int* d = p.docc + ((int64_t)b * p.Skv + j) * 2;
+    lo = d[0];
+    hi = d[1];
+  } else {
+    lo = 0;
+    hi = 0x7fffffff;
+  }
+}
+// Block-sparse mask: whether the 128 x 128 block holding (query row i, key j)
+// of head hq is computed (true when no block map is set).
+constexpr int kBlk = 128;
+constexpr int kBlkRowMax = 2048;  // KV blocks a kernel keeps of one block-map row (Skv <= 256 Ki)
+__device__ __forceinline__ const unsigned char* block_row(const Shape& p, int b, int hq, int i) {
+  return p.blk + ((int64_t)(b * p.blk_h + (p.blk_h > 1 ? hq : 0)) * p.blk_nq + i / kBlk) * p.blk_nk;
+}
+__device__ __forceinline__ bool block_on(const Shape& p, int b, int hq, int i, int j) {
+  return !p.blk || block_row(p, b, hq, i)[j / kBlk] != 0;
 }
 
 // --- staged dS (the D = 128 backward) -----------------------------------------

@@ -126,6 +126,19 @@ void fwd_mfma_kernel(FwdArgs a) {
   const int t_lo = kv_lo / C::BN;
   const int t_hi = (kv_hi + C::BN - 1) / C::BN;
 
+  // Block-sparse mask: this wave's row of the block map over the
+  // workgroup's KV range, kept in (dynamic) LDS so that the tile loop issues
+  // no memory operation besides its tile copies.
+  extern __shared__ unsigned char sblk[];
+  const int kb_base = t_lo * C::BN / kBlk;
+  if (p.blk && t_lo < t_hi) {
+    const unsigned char* row = block_row(p, b, hq, min(mw, p.Sq - 1));
+    const int nkb = (t_hi * C::BN - 1) / kBlk - kb_base + 1;
+    for (int i = lane; i < nkb; i += 64) sblk[wave * kBlkRowMax + i] = row[kb_base + i];
+  }
+  // whether the 128 x 128 block of this wave's rows and KV row n0 is computed
+  auto block_live = [&](int n0) { return !p.blk || sblk[wave * kBlkRowMax + n0 / kBlk - kb_base] != 0; };
+
   // Direct global -> LDS copy of tile t into stage st: E 1 KB loads per
   // tensor per wave; lane l of load e covers physical chunk q of the tile.
   const unsigned lds0 = lds_addr_of(smem);
@@ -208,12 +221,13 @@ void fwd_mfma_kernel(FwdArgs a) {
         }
     }
     if (need_mask) {
+      const bool live = block_live(n0);
 #pragma unroll
       for (int bb = 0; bb < C::NB; ++bb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (!allowed(p, my_m, j) || j < dlo || j >= dhi) s[bb][r] = kNegInf;
+          if (!live || !allowed(p, my_m, j) || j < dlo || j >= dhi) s[bb][r] = kNegInf;
         }
     }
 
@@ -342,16 +356,13 @@ void fwd_mfma_kernel(FwdArgs a) {
     if (p.causal) tm_hi = min(tm_hi, (mw + 1) / C::BN);  // n0 + BN - 1 <= mw
     int tm_lo = 0;
     if (p.window > 0) tm_lo = max(0, (mw + 31 - p.window + C::BN - 1) / C::BN);  // mw + 31 - n0 <= window
-    if (p.doc) {  // full tiles lie inside the one document of all the wave's rows
-      int l0, h0, l1, h1;
+    if (p.doc) {  // full tiles lie inside the key interval of every row of the wave:
+      int l0, h0, l1, h1;  // [lo of its last row, hi of its first row) (bounds are non-decreasing)
       doc_bounds(p, b, min(mw, p.Sq - 1), l0, h0);
       doc_bounds(p, b, min(mw + 31, p.Sq - 1), l1, h1);
-      if (l0 == l1) {
-        tm_lo = max(tm_lo, (l0 + C::BN - 1) / C::BN);
-        tm_hi = min(tm_hi, h0 / C::BN);
-      } else {
-        tm_hi = tm_lo;
-      }
+      tm_lo = max(tm_lo, (l1 + C::BN - 1) / C::BN);
+      tm_hi = min(tm_hi, h0 / C::BN);
+      if (tm_hi < tm_lo) tm_hi = tm_lo;
     }
     tm_hi = __builtin_amdgcn_readfirstlane(tm_hi);
     tm_lo = __builtin_amdgcn_readfirstlane(tm_lo);
@@ -369,13 +380,14 @@ void fwd_mfma_kernel(FwdArgs a) {
           }
       }
       const int tn = n0 / C::BN;
-      if (tn < tm_lo || tn >= tm_hi) {
+      const bool live = block_live(n0);
+      if (tn < tm_lo || tn >= tm_hi || !live) {
 #pragma unroll
         for (int bb = 0; bb < C::NB; ++bb) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (!allowed(p, my_m, j) || j < dlo || j >= dhi) s[bb][r] = kNegInf;
+            if (!live || !allowed(p, my_m, j) || j < dlo || j >= dhi) s[bb][r] = kNegInf;
           }
           pin(s[bb]);  // finished inside the branch (no selects after it)
         }
@@ -518,7 +530,7 @@ void fwd_mfma_kernel(FwdArgs a) {
       // Per element masking only on tiles that cut the causal diagonal, the
       // window edge or the KV tail for some row of this wave.
       const bool need_mask = (n0 + C::BN > p.Skv) || (p.causal && n0 + C::BN - 1 > mw) ||
-                             (p.window > 0 && mw + 31 - n0 > p.window) || p.doc;
+                             (p.window > 0 && mw + 31 - n0 > p.window) || p.doc || !block_live(n0);
       tile_body(sK, sV, n0, need_mask);
       st = st == 2 ? 0 : st + 1;
     }
@@ -557,10 +569,11 @@ hipError_t launch_fwd_mfma(const FwdArgs& a, hipStream_t st) {
   x.nqt = (a.p.Sq + bmh - 1) / bmh;
   const dim3 grid(x.nqt * (a.p.G / x.gpack) * a.p.B * a.p.Hkv), block(C::NW * 64);
   const bool sc = a.p.cap > 0.f, al = a.p.alibi != nullptr;
-  if (sc && al) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true, true>), grid, block, 0, st, x);
-  else if (sc) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true, false>), grid, block, 0, st, x);
-  else if (al) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false, true>), grid, block, 0, st, x);
-  else hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false, false>), grid, block, 0, st, x);
+  const size_t dyn = a.p.blk ? (size_t)C::NW * kBlkRowMax : 0;  // block-map rows
+  if (sc && al) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true, true>), grid, block, dyn, st, x);
+  else if (sc) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true, false>), grid, block, dyn, st, x);
+  else if (al) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false, true>), grid, block, dyn, st, x);
+  else hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false, false>), grid, block, dyn, st, x);
   return hipGetLastError();
 }
 

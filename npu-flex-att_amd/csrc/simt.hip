@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void fwd_simt_kernel(FwdArgs a) {
       const int j = n0 + jj;
       float t;
       float x = score(part, p, slope, my_m, j, t);
-      if (!allowed(p, my_m, j) || j < dlo || j >= dhi) x = kNegInf;
+      if (!allowed(p, my_m, j) || j < dlo || j >= dhi || !block_on(p, b, hq, min(my_m, p.Sq - 1), j)) x = kNegInf;
       sc[jj] = x;
       mx = fmaxf(mx, x);
     }
@@ -190,7 +190,9 @@ __global__ __launch_bounds__(256) void bwd_dq_simt_kernel(BwdArgs a) {
       const int j = n0 + jj;
       float t = 0.f;
       const float x = score(s, p, slope, my_m, j, t);
-      const float pj = (allowed(p, my_m, j) && j >= dlo && j < dhi) ? expf(x - lse) : 0.f;
+      const float pj = (allowed(p, my_m, j) && j >= dlo && j < dhi && block_on(p, b, hq, min(my_m, p.Sq - 1), j))
+                           ? expf(x - lse)
+                           : 0.f;
       float ds = pj * (dpv - dl) * p.scale;
       if (p.cap > 0.f) ds *= (1.0f - t * t);
 #pragma unroll
@@ -228,12 +230,12 @@ __global__ __launch_bounds__(256) void bwd_dkdv_simt_kernel(BwdArgs a) {
   }
   int q_lo = p.causal ? n0 : 0, q_hi = p.Sq;
   if (p.window > 0) q_hi = min(q_hi, n0 + kRows + p.window);
-  int dlo, dhi;  // document masks are symmetric: the query range of this KV row
-  doc_bounds(p, b, rn, dlo, dhi);
-  if (p.doc) {
+  int dlo, dhi;  // interval masks: the query range of this KV row (column bounds)
+  col_bounds(p, b, rn, dlo, dhi);
+  if (p.docc) {
     int l0, h0, l1, h1;
-    doc_bounds(p, b, min(n0, p.Skv - 1), l0, h0);
-    doc_bounds(p, b, min(n0 + kRows, p.Skv) - 1, l1, h1);
+    col_bounds(p, b, min(n0, p.Skv - 1), l0, h0);
+    col_bounds(p, b, min(n0 + kRows, p.Skv) - 1, l1, h1);
     q_lo = max(q_lo, l0);
     q_hi = min(q_hi, h1);
   }
@@ -275,7 +277,9 @@ __global__ __launch_bounds__(256) void bwd_dkdv_simt_kernel(BwdArgs a) {
         const int m = m0 + ii;
         float t = 0.f;
         const float x = score(s, p, slope, m, my_n, t);
-        const float pj = (m < p.Sq && allowed(p, m, my_n) && m >= dlo && m < dhi) ? expf(x - sL[ii]) : 0.f;
+        const float pj = (m < p.Sq && allowed(p, m, my_n) && m >= dlo && m < dhi && block_on(p, b, hq, m, my_n))
+                             ? expf(x - sL[ii])
+                             : 0.f;
         float ds = pj * (dpv - sDl[ii]) * p.scale;
         if (p.cap > 0.f) ds *= (1.0f - t * t);
 #pragma unroll

@@ -32,7 +32,7 @@ EXPORTS = (
     "flexatt_status_string",
     "flexatt_abi_version",
 )
-ABI_VERSION = 5
+ABI_VERSION = 6
 # Fixed scratch of flexatt_fwd_decode_noalloc (FLEXATT_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = 16 << 20
 
@@ -66,6 +66,10 @@ class Problem(ctypes.Structure):
         ("soft_cap", ctypes.c_float),
         ("alibi_slopes", ctypes.c_void_p),
         ("doc_bounds", ctypes.c_void_p),
+        ("col_bounds", ctypes.c_void_p),
+        ("block_map", ctypes.c_void_p),
+        ("block_heads", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 

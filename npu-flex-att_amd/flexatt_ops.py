@@ -7,11 +7,14 @@ registers the same forward / backward as two custom operators with fake
 keeps the HIP kernels as single nodes and traces around them without a graph
 break:
 
-  flexatt::fwd(q, k, v, alibi, scale, causal, window, soft_cap, doc) -> (O, LSE)
-  flexatt::bwd(dO, q, k, v, O, LSE, alibi, scale, causal, window, soft_cap, doc)
-      -> (dQ, dK, dV)
+  flexatt::fwd(q, k, v, alibi, scale, causal, window, soft_cap, rows, cols, blocks)
+      -> (O, LSE)
+  flexatt::bwd(dO, q, k, v, O, LSE, alibi, scale, causal, window, soft_cap, rows, cols,
+               blocks) -> (dQ, dK, dV)
 
-(``doc``: optional int32 [B, S, 2] document bounds, see ``document_ids``.)
+(``rows`` / ``cols``: optional int32 [B, Sq, 2] / [B, Skv, 2] interval bounds,
+``blocks``: optional uint8 block map, as built from ``document_ids``,
+``prefix_len`` and ``block_mask`` by the npu_flash_attention entry points.)
 
 Both run exactly the kernels of npu_flash_attention_forward / _backward
 (npu_flash_attention.py:606-656, :659-739 in the reference), so results are
@@ -52,17 +55,24 @@ def _check_shapes(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
 @torch.library.custom_op(f"{_NS}::fwd", mutates_args=(), device_types="cuda")
 def _fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, alibi: Optional[torch.Tensor],
          scale: float, causal: bool, window: int, soft_cap: float,
-         doc: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+         rows: Optional[torch.Tensor] = None, cols: Optional[torch.Tensor] = None,
+         blocks: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     _check_shapes(q, k, v)
     O = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     LSE = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
     _nfa._forward_into(q, k, v, O, LSE, causal=causal, sliding_window=window, alibi=alibi,
-                       scale=scale, soft_cap=soft_cap, doc=doc)
+                       scale=scale, soft_cap=soft_cap, masks=_as_masks(causal, rows, cols, blocks))
     return O, LSE
 
 
+def _as_masks(causal, rows, cols, blocks):
+    if rows is None and cols is None and blocks is None:
+        return None
+    return _nfa._Masks(causal, rows, cols, blocks)
+
+
 @_fwd.register_fake
-def _fwd_fake(q, k, v, alibi, scale, causal, window, soft_cap, doc=None):
+def _fwd_fake(q, k, v, alibi, scale, causal, window, soft_cap, rows=None, cols=None, blocks=None):
     _check_shapes(q, k, v)
     return q.new_empty(q.shape), q.new_empty(q.shape[:3], dtype=torch.float32)
 
@@ -70,34 +80,35 @@ def _fwd_fake(q, k, v, alibi, scale, causal, window, soft_cap, doc=None):
 @torch.library.custom_op(f"{_NS}::bwd", mutates_args=(), device_types="cuda")
 def _bwd(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
          lse: torch.Tensor, alibi: Optional[torch.Tensor], scale: float, causal: bool, window: int,
-         soft_cap: float, doc: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+         soft_cap: float, rows: Optional[torch.Tensor] = None, cols: Optional[torch.Tensor] = None,
+         blocks: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     _check_shapes(q, k, v)
     DQ = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     DK = torch.empty(k.shape, dtype=k.dtype, device=k.device)
     DV = torch.empty(v.shape, dtype=v.dtype, device=v.device)
     _nfa._backward_into(q, k, v, o, lse, do, DQ, DK, DV, causal=causal, sliding_window=window,
-                        alibi=alibi, scale=scale, soft_cap=soft_cap, doc=doc)
+                        alibi=alibi, scale=scale, soft_cap=soft_cap, masks=_as_masks(causal, rows, cols, blocks))
     return DQ, DK, DV
 
 
 @_bwd.register_fake
-def _bwd_fake(do, q, k, v, o, lse, alibi, scale, causal, window, soft_cap, doc=None):
+def _bwd_fake(do, q, k, v, o, lse, alibi, scale, causal, window, soft_cap, rows=None, cols=None, blocks=None):
     _check_shapes(q, k, v)
     return q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape)
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, alibi, scale, causal, window, soft_cap, doc = inputs
+    q, k, v, alibi, scale, causal, window, soft_cap, rows, cols, blocks = inputs
     o, lse = output
     ctx.mark_non_differentiable(lse)
-    ctx.save_for_backward(q, k, v, o, lse, alibi, doc)
+    ctx.save_for_backward(q, k, v, o, lse, alibi, rows, cols, blocks)
     ctx.params = (scale, causal, window, soft_cap)
 
 
 def _backward(ctx, do, dlse):
-    q, k, v, o, lse, alibi, doc = ctx.saved_tensors
-    dq, dk, dv = torch.ops.flexatt.bwd(do.contiguous(), q, k, v, o, lse, alibi, *ctx.params, doc)
-    return dq, dk, dv, None, None, None, None, None, None
+    q, k, v, o, lse, alibi, rows, cols, blocks = ctx.saved_tensors
+    dq, dk, dv = torch.ops.flexatt.bwd(do.contiguous(), q, k, v, o, lse, alibi, *ctx.params, rows, cols, blocks)
+    return dq, dk, dv, None, None, None, None, None, None, None, None
 
 
 torch.library.register_autograd(f"{_NS}::fwd", _backward, setup_context=_setup_context)
@@ -105,12 +116,15 @@ torch.library.register_autograd(f"{_NS}::fwd", _backward, setup_context=_setup_c
 
 def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, causal: bool = False,
               sliding_window: int = 0, alibi_slope=None, scale: Optional[float] = None,
-              soft_cap: float = 0.0, document_ids: Optional[torch.Tensor] = None) -> torch.Tensor:
+              soft_cap: float = 0.0, document_ids: Optional[torch.Tensor] = None,
+              prefix_len=None, block_mask=None) -> torch.Tensor:
     """Differentiable attention through the registered operators; returns O.
 
     Same arguments and defaults as ``npu_flex_attention`` (default scale
     ``1/sqrt(D)``, primitives enabled by positive values, optional
-    ``document_ids``); usable inside ``torch.compile(fullgraph=True)``.
+    ``document_ids``, ``prefix_len`` and ``block_mask``); usable inside
+    ``torch.compile(fullgraph=True)`` with mask arguments built outside the
+    compiled region or absent.
     """
     if scale is None:
         scale = 1.0 / math.sqrt(query.shape[-1])
@@ -119,9 +133,11 @@ def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, causa
         alibi = torch.as_tensor(alibi_slope, dtype=torch.float32, device=query.device).reshape(-1)
     window = int(sliding_window) if sliding_window and sliding_window > 0 else 0
     cap = float(soft_cap) if soft_cap and soft_cap > 0.0 else 0.0
-    doc = None
-    if document_ids is not None:
-        B, _, Sq, _ = query.shape
-        doc = _nfa._doc_bounds(document_ids, B, Sq, key.shape[2], query.device)
-    o, _ = torch.ops.flexatt.fwd(query, key, value, alibi, float(scale), bool(causal), window, cap, doc)
+    B, Hq, Sq, _ = query.shape
+    m = _nfa._masks(causal, document_ids, prefix_len, block_mask, B, Hq, Sq, key.shape[2], query.device)
+    if m is None:
+        o, _ = torch.ops.flexatt.fwd(query, key, value, alibi, float(scale), bool(causal), window, cap)
+    else:
+        o, _ = torch.ops.flexatt.fwd(query, key, value, alibi, float(scale), m.causal, window, cap,
+                                     m.rows, m.cols, m.blocks)
     return o

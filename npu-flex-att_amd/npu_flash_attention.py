@@ -19,6 +19,19 @@ Public API (reference file:line):
 ``block_m`` / ``block_n`` are accepted for signature compatibility; they were
 tiling hints of the Triton kernels and do not change results here (the HIP
 kernels use fixed gfx950 tilings).
+
+Masks beyond the reference's primitives (its README.md:198, :219 and
+DESIGN.md:374 list them as unsupported or future work), on every entry point:
+
+* ``document_ids`` [B, S]: positions of different runs of equal ids do not
+  attend to each other;
+* ``prefix_len`` (int or [B]): PrefixLM, with ``causal``; keys below the
+  prefix are visible to every query row, the rest stay causal;
+* ``block_mask``: block-sparse mask over 128 x 128 blocks of (query rows,
+  keys), given as a dense block map [B|1, Hq|1, ceil(Sq/128), ceil(Skv/128)]
+  (bool or integer), as ``(kv_num_blocks, kv_indices)`` index tensors, or as
+  a ``torch.nn.attention.flex_attention.BlockMask`` with BLOCK_SIZE 128 whose
+  listed blocks are whole (no ``mask_mod`` other than the no-op).
 """
 from __future__ import annotations
 
@@ -46,10 +59,11 @@ _DTYPES = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _li
 # Set to False to force the regular forward kernel (tests compare the two).
 decode_enabled = True
 # The backward stages dS through a workspace (flexatt_bwd_ws) whenever the
-# library supports it for the problem (fp16/bf16, head_dim 128, no document
-# mask).  Set to False to run the recomputing dQ kernel (flexatt_bwd).
+# library supports it for the problem (fp16/bf16, head_dim 128).  Set to
+# False to run the recomputing dQ kernel (flexatt_bwd).
 ds_staging_enabled = True
 _HEAD_DIMS = (32, 64, 128, 256)
+_BLOCK = 128  # block edge of the block-sparse map (flexatt_problem.block_map)
 
 
 # ----------------------------------------------------------------- helpers --
@@ -78,7 +92,19 @@ def _check_device_dtype(name_tensors, dtype):
             raise RuntimeError(f"{name} has dtype {t.dtype}, expected {dtype}")
 
 
-def _problem(query, key, scale, causal, sliding_window, soft_cap, alibi, doc=None):
+class _Masks:
+    """Device tensors of the interval and block masks of one call (kept alive
+    for the duration of the kernels) and the causal flag the kernels see:
+    PrefixLM is encoded in the row / column bounds with the flag cleared."""
+
+    __slots__ = ("causal", "rows", "cols", "blocks")
+
+    def __init__(self, causal, rows=None, cols=None, blocks=None):
+        self.causal = bool(causal)
+        self.rows, self.cols, self.blocks = rows, cols, blocks
+
+
+def _problem(query, key, scale, causal, sliding_window, soft_cap, alibi, masks=None):
     B, Hq, Sq, D = query.shape
     Hkv, Sk = key.shape[1], key.shape[2]
     if query.dtype not in _DTYPES:
@@ -89,13 +115,20 @@ def _problem(query, key, scale, causal, sliding_window, soft_cap, alibi, doc=Non
     p.dtype = _DTYPES[query.dtype]
     p.batch, p.heads_q, p.heads_kv, p.seqlen_q, p.seqlen_kv, p.head_dim = B, Hq, Hkv, Sq, Sk, D
     p.scale = float(scale)
+    if masks is not None:
+        causal = masks.causal
     p.causal = 1 if causal else 0
     # The reference enables a primitive only for a positive value
     # (npu_flash_attention.py:70, :648).
     p.sliding_window = int(sliding_window) if sliding_window and sliding_window > 0 else 0
     p.soft_cap = float(soft_cap) if soft_cap and soft_cap > 0.0 else 0.0
     p.alibi_slopes = alibi.data_ptr() if alibi is not None else None
-    p.doc_bounds = doc.data_ptr() if doc is not None else None
+    if masks is not None:
+        p.doc_bounds = masks.rows.data_ptr() if masks.rows is not None else None
+        p.col_bounds = masks.cols.data_ptr() if masks.cols is not None else None
+        if masks.blocks is not None:
+            p.block_map = masks.blocks.data_ptr()
+            p.block_heads = masks.blocks.shape[1]
     return p
 
 
@@ -131,6 +164,112 @@ def _doc_bounds(document_ids, B, Sq, Sk, device):
     return torch.stack((lo, hi), dim=-1).to(torch.int32).contiguous()
 
 
+def _prefix_bounds(prefix_len, doc, B, Sq, Sk, device):
+    """PrefixLM with causal: query row i sees keys j <= i and every key
+    j < P[b], i.e. the keys [0, max(i + 1, P)); key j is seen by the rows
+    [0, Sq) when j < P, else [j, Sq).  Intersected with the document bounds
+    ``doc`` (symmetric, Sq == Skv) when given.  Returns int32 row bounds
+    [B, Sq, 2] and column bounds [B, Skv, 2], both non-decreasing."""
+    pl = torch.as_tensor(prefix_len, device=device)
+    if pl.dtype.is_floating_point or pl.dtype == torch.bool:
+        raise RuntimeError("prefix_len must be an int or an integer tensor")
+    pl = pl.reshape(-1).to(torch.int64)
+    if pl.numel() == 1:
+        pl = pl.expand(B)
+    if pl.numel() != B:
+        raise RuntimeError(f"prefix_len must be an int or have B={B} entries, got {pl.numel()}")
+    pl = pl.clamp(0, Sk).view(B, 1)
+    i = torch.arange(Sq, device=device, dtype=torch.int64).view(1, Sq)
+    j = torch.arange(Sk, device=device, dtype=torch.int64).view(1, Sk)
+    r_lo = torch.zeros(B, Sq, dtype=torch.int64, device=device)
+    r_hi = torch.maximum(i + 1, pl).clamp(max=Sk)
+    c_lo = torch.where(j < pl, torch.zeros_like(j), j).expand(B, Sk)
+    c_hi = torch.full((B, Sk), Sq, dtype=torch.int64, device=device)
+    if doc is not None:
+        r_lo = torch.maximum(r_lo, doc[..., 0])
+        r_hi = torch.minimum(r_hi, doc[..., 1])
+        c_lo = torch.maximum(c_lo, doc[..., 0])
+        c_hi = torch.minimum(c_hi, doc[..., 1])
+    rows = torch.stack((r_lo, r_hi), dim=-1).to(torch.int32).contiguous()
+    cols = torch.stack((c_lo, c_hi), dim=-1).to(torch.int32).contiguous()
+    return rows, cols
+
+
+def _dense_blocks(num, idx, nk, name):
+    """(kv_num_blocks [.., nq], kv_indices [.., nq, K]) -> bool [.., nq, nk]:
+    the first num[...] entries of each index row are the listed blocks."""
+    if num.dtype.is_floating_point or idx.dtype.is_floating_point:
+        raise RuntimeError(f"{name}: kv_num_blocks / kv_indices must be integer tensors")
+    if idx.dim() != num.dim() + 1 or idx.shape[:-1] != num.shape:
+        raise RuntimeError(f"{name}: kv_indices {tuple(idx.shape)} does not extend kv_num_blocks {tuple(num.shape)}")
+    K = idx.shape[-1]
+    idx = idx.to(torch.int64)
+    listed = torch.arange(K, device=idx.device) < num.to(torch.int64).unsqueeze(-1)
+    if bool(((idx < 0) | (idx >= nk))[listed].any()):
+        raise RuntimeError(f"{name}: a listed block index is outside [0, {nk})")
+    out = torch.zeros(*num.shape, nk + 1, dtype=torch.bool, device=idx.device)
+    out.scatter_(-1, torch.where(listed, idx, nk), True)  # unlisted slots land in a spare column
+    return out[..., :nk]
+
+
+def _block_map(block_mask, B, Hq, Sq, Sk, device):
+    """A block mask in any accepted form -> contiguous uint8 block map
+    [B, Hm, ceil(Sq/128), ceil(Skv/128)] on ``device`` with Hm in {1, Hq}."""
+    nq, nk = -(-Sq // _BLOCK), -(-Sk // _BLOCK)
+    if isinstance(block_mask, torch.Tensor):
+        m = block_mask
+        if m.dtype.is_floating_point:
+            raise RuntimeError("a dense block_mask must be bool or integer")
+        if m.dim() != 4 or m.shape[2] != nq or m.shape[3] != nk:
+            raise RuntimeError(f"a dense block_mask must be [B|1, Hq|1, {nq}, {nk}] (blocks of {_BLOCK}), "
+                               f"got {tuple(m.shape)}")
+        m = m != 0
+    else:
+        if isinstance(block_mask, (tuple, list)) and len(block_mask) == 2:
+            parts = [tuple(block_mask)]
+        elif hasattr(block_mask, "kv_num_blocks") and hasattr(block_mask, "kv_indices"):
+            bs = getattr(block_mask, "BLOCK_SIZE", (_BLOCK, _BLOCK))
+            bs = tuple(bs) if isinstance(bs, (tuple, list)) else (bs, bs)
+            if bs != (_BLOCK, _BLOCK):
+                raise RuntimeError(f"block_mask BLOCK_SIZE must be ({_BLOCK}, {_BLOCK}), got {bs}")
+            parts = [(block_mask.kv_num_blocks, block_mask.kv_indices)]
+            mm = getattr(block_mask, "mask_mod", None)
+            partial = bool((block_mask.kv_num_blocks != 0).any())
+            if partial and mm is not None and getattr(mm, "__name__", "") != "noop_mask":
+                raise RuntimeError("block_mask: mask_mod functions are not supported; "
+                                   "only whole blocks (no mask_mod, or full_kv_* blocks)")
+            if getattr(block_mask, "full_kv_num_blocks", None) is not None:
+                parts.append((block_mask.full_kv_num_blocks, block_mask.full_kv_indices))
+        else:
+            raise RuntimeError("block_mask must be a dense block map tensor, a (kv_num_blocks, kv_indices) "
+                               "pair or a BlockMask")
+        m = None
+        for num, idx in parts:
+            d = _dense_blocks(torch.as_tensor(num, device=device), torch.as_tensor(idx, device=device), nk,
+                              "block_mask")
+            if d.dim() != 4 or d.shape[2] < nq:
+                raise RuntimeError(f"block_mask must list blocks for [B|1, Hq|1, >= {nq}] query blocks, "
+                                   f"got {tuple(d.shape[:3])}")
+            d = d[:, :, :nq]
+            m = d if m is None else (m | d)
+    if m.shape[0] not in (1, B) or m.shape[1] not in (1, Hq):
+        raise RuntimeError(f"block_mask must have batch 1 or {B} and heads 1 or {Hq}, got {tuple(m.shape[:2])}")
+    return m.to(device=device, dtype=torch.uint8).expand(B, m.shape[1], nq, nk).contiguous()
+
+
+def _masks(causal, document_ids, prefix_len, block_mask, B, Hq, Sq, Sk, device):
+    """The interval / block masks of one call as kernel inputs, or None."""
+    if document_ids is None and block_mask is None and (prefix_len is None or not causal):
+        return None
+    rows = _doc_bounds(document_ids, B, Sq, Sk, device)
+    cols = None
+    if prefix_len is not None and causal:
+        rows, cols = _prefix_bounds(prefix_len, rows, B, Sq, Sk, device)
+        causal = False
+    blocks = _block_map(block_mask, B, Hq, Sq, Sk, device) if block_mask is not None else None
+    return _Masks(causal, rows, cols, blocks)
+
+
 def _stream(device):
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -147,15 +286,17 @@ def npu_flash_attention_forward(
     return_lse=False,
     soft_cap=0.0,
     document_ids=None,
+    prefix_len=None,
+    block_mask=None,
 ):
     """Attention forward; returns ``O`` or ``(O, LSE)``.
 
     ``O`` has ``query``'s dtype and layout (``empty_like``), ``LSE`` is fp32
     ``[B, Hq, Sq]`` in natural log.  Follows npu_flash_attention.py:606-656:
     the same shape assertions (:620-622) and default scale ``1/sqrt(D)``
-    (:625-626).  ``document_ids`` ([B, S] integers, Sq == Skv; no counterpart
-    in the reference) adds a document mask: positions of different runs of
-    equal ids do not attend to each other.
+    (:625-626).  ``document_ids`` ([B, S] integers, Sq == Skv), ``prefix_len``
+    and ``block_mask`` add the masks described in the module docstring (no
+    counterpart in the reference).
     """
     B, Hq, Sq, D = query.shape
     Bk, Hkv, Sk, Dk = key.shape
@@ -174,15 +315,15 @@ def npu_flash_attention_forward(
     if not _kernel_ready(O):
         O = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     LSE = torch.empty(B, Hq, Sq, device=query.device, dtype=torch.float32)
-    doc = _doc_bounds(document_ids, B, Sq, Sk, query.device)
+    masks = _masks(causal, document_ids, prefix_len, block_mask, B, Hq, Sq, Sk, query.device)
     _forward_into(query, key, value, O, LSE, causal=causal, sliding_window=sliding_window,
-                  alibi=alibi_slope, scale=scale, soft_cap=soft_cap, doc=doc)
+                  alibi=alibi_slope, scale=scale, soft_cap=soft_cap, masks=masks)
     if return_lse:
         return O, LSE
     return O
 
 
-def _forward_into(query, key, value, O, LSE, *, causal, sliding_window, alibi, scale, soft_cap, doc=None):
+def _forward_into(query, key, value, O, LSE, *, causal, sliding_window, alibi, scale, soft_cap, masks=None):
     """Run the forward kernels into the caller's ``O`` (kernel-ready layout)
     and contiguous fp32 ``LSE``; shapes are already validated."""
     if O.numel() == 0 or key.shape[2] == 0:
@@ -192,7 +333,7 @@ def _forward_into(query, key, value, O, LSE, *, causal, sliding_window, alibi, s
     lib = _lib.load()
     q, k, v = _prepare(query), _prepare(key), _prepare(value)
     slopes = _alibi(alibi, query.shape[1], query.device)
-    p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes, doc)
+    p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes, masks)
     # Few query rows per KV head (decoding): the split-KV kernels, with their
     # partial results in a workspace from torch's caching allocator.
     ws_bytes = lib.flexatt_fwd_decode_workspace(p) if decode_enabled else 0
@@ -219,6 +360,8 @@ def npu_flash_attention_backward(
     block_n=32,
     soft_cap=0.0,
     document_ids=None,
+    prefix_len=None,
+    block_mask=None,
 ):
     """Attention backward; returns ``(dQ, dK, dV)``.
 
@@ -248,14 +391,14 @@ def npu_flash_attention_backward(
         DQ = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     DK = torch.empty(B, Hkv, Sk, D, device=key.device, dtype=key.dtype)
     DV = torch.empty(B, Hkv, Sk, D, device=value.device, dtype=value.dtype)
-    doc = _doc_bounds(document_ids, B, Sq, Sk, query.device)
+    masks = _masks(causal, document_ids, prefix_len, block_mask, B, Hq, Sq, Sk, query.device)
     _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, causal=causal,
-                   sliding_window=sliding_window, alibi=alibi_slope, scale=scale, soft_cap=soft_cap, doc=doc)
+                   sliding_window=sliding_window, alibi=alibi_slope, scale=scale, soft_cap=soft_cap, masks=masks)
     return DQ, DK, DV
 
 
 def _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, *, causal, sliding_window,
-                   alibi, scale, soft_cap, doc=None):
+                   alibi, scale, soft_cap, masks=None):
     """Run Delta, dQ and dK/dV into the caller's ``DQ`` (kernel-ready layout)
     and contiguous ``DK`` / ``DV``; shapes are already validated."""
     if DQ.numel() == 0 or DK.numel() == 0:
@@ -270,7 +413,7 @@ def _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, *, causal,
     o, do = _prepare(out), _prepare(grad_out)
     lse = lse.to(torch.float32).contiguous()
     slopes = _alibi(alibi, Hq, query.device)
-    p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes, doc)
+    p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes, masks)
     # head_dim 128 fp16/bf16: the dK/dV kernel stages its dS in a workspace
     # from torch's caching allocator and dQ is formed from it
     ws_bytes = lib.flexatt_bwd_workspace(p) if ds_staging_enabled else 0
@@ -299,7 +442,8 @@ class NPUFlexAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, query, key, value, causal=False, sliding_window=0,
-                alibi_slope=None, scale=None, block_m=16, block_n=64, soft_cap=0.0, document_ids=None):
+                alibi_slope=None, scale=None, block_m=16, block_n=64, soft_cap=0.0, document_ids=None,
+                prefix_len=None, block_mask=None):
         ctx.causal = causal
         ctx.sliding_window = sliding_window
         ctx.alibi_slope = alibi_slope
@@ -308,6 +452,8 @@ class NPUFlexAttention(torch.autograd.Function):
         ctx.block_n = block_n
         ctx.soft_cap = soft_cap
         ctx.document_ids = document_ids
+        ctx.prefix_len = prefix_len
+        ctx.block_mask = block_mask
         with torch.no_grad():
             out, lse = npu_flash_attention_forward(
                 query, key, value,
@@ -315,6 +461,7 @@ class NPUFlexAttention(torch.autograd.Function):
                 alibi_slope=alibi_slope, scale=scale,
                 block_m=block_m, block_n=block_n, return_lse=True,
                 soft_cap=soft_cap, document_ids=document_ids,
+                prefix_len=prefix_len, block_mask=block_mask,
             )
         ctx.save_for_backward(query, key, value, lse, out)
         return out
@@ -328,8 +475,9 @@ class NPUFlexAttention(torch.autograd.Function):
             alibi_slope=ctx.alibi_slope, scale=ctx.scale,
             block_m=ctx.block_m, block_n=ctx.block_n,
             soft_cap=ctx.soft_cap, document_ids=ctx.document_ids,
+            prefix_len=ctx.prefix_len, block_mask=ctx.block_mask,
         )
-        return DQ, DK, DV, None, None, None, None, None, None, None, None
+        return DQ, DK, DV, None, None, None, None, None, None, None, None, None, None
 
 
 def npu_flex_attention(
@@ -339,12 +487,14 @@ def npu_flex_attention(
     block_m=16, block_n=64,
     soft_cap=0.0,
     document_ids=None,
+    prefix_len=None,
+    block_mask=None,
 ):
-    """Autograd entry point (npu_flash_attention.py:784-794); ``document_ids``
-    as in :func:`npu_flash_attention_forward`."""
+    """Autograd entry point (npu_flash_attention.py:784-794); ``document_ids``,
+    ``prefix_len`` and ``block_mask`` as in :func:`npu_flash_attention_forward`."""
     return NPUFlexAttention.apply(
         query, key, value, causal, sliding_window,
-        alibi_slope, scale, block_m, block_n, soft_cap, document_ids,
+        alibi_slope, scale, block_m, block_n, soft_cap, document_ids, prefix_len, block_mask,
     )
 
 
@@ -370,13 +520,18 @@ class AttentionConfig:
     soft_cap: float = 0.0
     block_m: int = 16
     block_n: int = 64
-    document_ids: Optional[torch.Tensor] = None  # no counterpart in the reference
+    # no counterpart in the reference: document, PrefixLM and block masks
+    document_ids: Optional[torch.Tensor] = None
+    prefix_len: Optional[object] = None
+    block_mask: Optional[object] = None
 
     def __post_init__(self):
         if self.sliding_window < 0:
             raise ValueError("sliding_window must be >= 0")
         if self.soft_cap < 0:
             raise ValueError("soft_cap must be >= 0")
+        if self.prefix_len is not None and not self.causal:
+            raise ValueError("prefix_len relaxes the causal mask and needs causal=True")
 
 
 def flex_attention(query, key, value, config: Optional[AttentionConfig] = None, **kwargs):
@@ -398,4 +553,6 @@ def flex_attention(query, key, value, config: Optional[AttentionConfig] = None, 
         block_n=config.block_n,
         soft_cap=config.soft_cap,
         document_ids=config.document_ids,
+        prefix_len=config.prefix_len,
+        block_mask=config.block_mask,
     )

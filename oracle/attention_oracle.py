@@ -22,6 +22,10 @@ every primitive the kernels implement:
 * GQA: query head ``h`` reads KV head ``h // G`` (npu_flash_attention.py:42);
 * document masks (no counterpart in the reference, see :func:`document_mask`):
   pairs in different runs of ``document_ids`` are masked;
+* PrefixLM (see :func:`prefix_mask`): with ``causal``, keys below
+  ``prefix_len[b]`` are visible to every query row;
+* block maps (see :func:`block_mask_dense`): whole blocks of (query rows,
+  keys) removed from the attention;
 * backward: ``Delta = rowsum(O*dO)`` (npu_flash_attention.py:681-685),
   ``dS = P*(dP-Delta)*scale*(1-tanh^2)`` (npu_flash_attention.py:386-399,
   :502-516), dK/dV summed over the G query heads of a group
@@ -53,6 +57,8 @@ __all__ = [
     "forward_backward_chunked",
     "forward_backward_rows",
     "attention_pairs",
+    "prefix_mask",
+    "block_mask_dense",
 ]
 
 
@@ -91,10 +97,39 @@ def document_mask(document_ids: torch.Tensor) -> torch.Tensor:
     return (run.unsqueeze(-1) == run.unsqueeze(-2)).unsqueeze(1)
 
 
-def _mask(sq, skv, causal, sliding_window, document_ids):
-    ok = allowed_mask(sq, skv, causal, sliding_window)
+def prefix_mask(sq: int, skv: int, prefix_len) -> torch.Tensor:
+    """Boolean [B, 1, Sq, Skv] PrefixLM relaxation of the causal mask: key j
+    is visible to every query row when ``j < prefix_len[b]`` (a bidirectional
+    prefix), otherwise only to rows ``i >= j``.  PrefixLM has no counterpart
+    in the reference (a future candidate in its DESIGN.md:374); it replaces
+    the causal term of :func:`allowed_mask`, the other primitives still
+    apply."""
+    pl = torch.as_tensor(prefix_len).reshape(-1).to("cpu", torch.long)
+    i = torch.arange(sq).view(1, -1, 1)
+    j = torch.arange(skv).view(1, 1, -1)
+    return ((j <= i) | (j < pl.view(-1, 1, 1))).unsqueeze(1)
+
+
+def block_mask_dense(block_map: torch.Tensor, sq: int, skv: int, block_size: int = 128) -> torch.Tensor:
+    """Boolean [B, H, Sq, Skv] mask of a block map [B, H, ceil(Sq / bs),
+    ceil(Skv / bs)] (nonzero = block computed): pair (i, j) is kept when block
+    (i // bs, j // bs) is.  The reference lists block-sparse masks as
+    unsupported (README.md:198); here a block map only removes whole blocks,
+    on top of the other primitives."""
+    m = block_map.detach().to("cpu") != 0
+    m = m.repeat_interleave(block_size, dim=-2).repeat_interleave(block_size, dim=-1)
+    return m[..., :sq, :skv]
+
+
+def _mask(sq, skv, causal, sliding_window, document_ids, prefix_len=None, block_map=None, block_size=128):
+    if prefix_len is not None and causal:
+        ok = allowed_mask(sq, skv, False, sliding_window) & prefix_mask(sq, skv, prefix_len)
+    else:
+        ok = allowed_mask(sq, skv, causal, sliding_window)
     if document_ids is not None:
         ok = ok & document_mask(document_ids)
+    if block_map is not None:
+        ok = ok & block_mask_dense(block_map, sq, skv, block_size)
     return ok
 
 
@@ -166,6 +201,9 @@ def forward(
     soft_cap: float = 0.0,
     dtype: torch.dtype = torch.float64,
     document_ids: Optional[torch.Tensor] = None,
+    prefix_len=None,
+    block_map: Optional[torch.Tensor] = None,
+    block_size: int = 128,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Eager attention forward: returns (O [B,Hq,Sq,D], LSE [B,Hq,Sq]).
 
@@ -175,7 +213,7 @@ def forward(
     """
     qf, kf, vf, scale, _ = _prep(q, k, v, scale, dtype)
     x, _ = scores(qf, kf, scale, soft_cap, alibi_slope)
-    ok = _mask(x.shape[-2], x.shape[-1], causal, sliding_window, document_ids)
+    ok = _mask(x.shape[-2], x.shape[-1], causal, sliding_window, document_ids, prefix_len, block_map, block_size)
     p, lse = _softmax_masked(x, ok)
     return torch.matmul(p, vf), lse
 
@@ -185,13 +223,14 @@ def delta(o: torch.Tensor, do: torch.Tensor, dtype: torch.dtype = torch.float64)
     return (o.detach().to("cpu", dtype) * do.detach().to("cpu", dtype)).sum(-1)
 
 
-def _score_grad(qf, kf, vf, dof, causal, sliding_window, alibi_slope, scale, soft_cap, o, dtype, document_ids):
+def _score_grad(qf, kf, vf, dof, causal, sliding_window, alibi_slope, scale, soft_cap, o, dtype, document_ids,
+                prefix_len=None, block_map=None, block_size=128):
     """(dS / scale, P) [B, Hq, Sq, Skv] from prepared (expanded) inputs:
     ``P (dP - Delta) (1 - tanh^2)``, 0 at masked pairs (npu_flash_attention.py
     :386-397, :502-513)."""
     sq = qf.shape[2]
     x, t = scores(qf, kf, scale, soft_cap, alibi_slope)
-    ok = _mask(sq, x.shape[-1], causal, sliding_window, document_ids)
+    ok = _mask(sq, x.shape[-1], causal, sliding_window, document_ids, prefix_len, block_map, block_size)
     p, _ = _softmax_masked(x, ok)
     of = torch.matmul(p, vf) if o is None else o.detach().to("cpu", dtype)
     dl = (of * dof).sum(-1, keepdim=True)
@@ -203,7 +242,7 @@ def _score_grad(qf, kf, vf, dof, causal, sliding_window, alibi_slope, scale, sof
 
 
 def score_grad(q, k, v, do, causal=False, sliding_window=0, alibi_slope=None, scale=None, soft_cap=0.0,
-               dtype=torch.float64, document_ids=None):
+               dtype=torch.float64, document_ids=None, prefix_len=None, block_map=None, block_size=128):
     """Gradient of the loss with respect to the scaled, capped, biased logits
     before the scale factor: ``dS / scale = P (dP - Delta) (1 - tanh^2)``,
     [B, Hq, Sq, Skv], 0 at masked pairs.  :func:`backward` forms
@@ -211,7 +250,7 @@ def score_grad(q, k, v, do, causal=False, sliding_window=0, alibi_slope=None, sc
     it is pinned by backward's checks."""
     qf, kf, vf, scale, _ = _prep(q, k, v, scale, dtype)
     return _score_grad(qf, kf, vf, do.detach().to("cpu", dtype), causal, sliding_window, alibi_slope, scale,
-                       soft_cap, None, dtype, document_ids)[0]
+                       soft_cap, None, dtype, document_ids, prefix_len, block_map, block_size)[0]
 
 
 def backward(
@@ -227,6 +266,9 @@ def backward(
     dtype: torch.dtype = torch.float64,
     o: Optional[torch.Tensor] = None,
     document_ids: Optional[torch.Tensor] = None,
+    prefix_len=None,
+    block_map: Optional[torch.Tensor] = None,
+    block_size: int = 128,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Closed-form attention backward: (dQ, dK, dV), dK/dV in [B,Hkv,Skv,D].
 
@@ -243,7 +285,7 @@ def backward(
     qf, kf, vf, scale, g = _prep(q, k, v, scale, dtype)
     dof = do.detach().to("cpu", dtype)
     ds, p = _score_grad(qf, kf, vf, dof, causal, sliding_window, alibi_slope, scale, soft_cap, o, dtype,
-                        document_ids)
+                        document_ids, prefix_len, block_map, block_size)
     ds = ds * scale
     dq = torch.matmul(ds, kf)
     dk = torch.matmul(ds.transpose(-2, -1), qf)
@@ -255,7 +297,8 @@ def backward(
 
 
 def backward_autograd(q, k, v, do, causal=False, sliding_window=0, alibi_slope=None,
-                      scale=None, soft_cap=0.0, dtype=torch.float64, document_ids=None):
+                      scale=None, soft_cap=0.0, dtype=torch.float64, document_ids=None, prefix_len=None,
+                      block_map=None, block_size=128):
     """(dQ, dK, dV) by autograd through :func:`forward` — the form of the
     reference's oracle ``ref_sdpa_backward`` (test/test_comprehensive.py:54-60);
     GQA K/V gradients come out summed over the group because the expansion is
@@ -267,7 +310,7 @@ def backward_autograd(q, k, v, do, causal=False, sliding_window=0, alibi_slope=N
     g = hq // hkv
     sc = (1.0 / math.sqrt(q.shape[-1])) if scale is None else float(scale)
     x, _ = scores(qr, _expand_kv(kr, g), sc, soft_cap, alibi_slope)
-    ok = _mask(x.shape[-2], x.shape[-1], causal, sliding_window, document_ids)
+    ok = _mask(x.shape[-2], x.shape[-1], causal, sliding_window, document_ids, prefix_len, block_map, block_size)
     p, _ = _softmax_masked(x, ok)
     o = torch.matmul(p, _expand_kv(vr, g))
     o.backward(do.detach().to("cpu", dtype))

@@ -38,10 +38,12 @@ def test_abi_version_and_status_strings():
 
 
 def test_struct_layout_matches_header():
-    # flexatt_tensor: pointer + 4 x int64; flexatt_problem: 7 int32, float, 2 int32, float, 2 pointers
+    # flexatt_tensor: pointer + 4 x int64; flexatt_problem: 7 int32, float, 2 int32, float, 4 pointers,
+    # 2 int32
     assert ctypes.sizeof(L.Tensor) == 40
     assert L.Problem.alibi_slopes.offset == 48 and L.Problem.doc_bounds.offset == 56
-    assert ctypes.sizeof(L.Problem) == 64
+    assert L.Problem.col_bounds.offset == 64 and L.Problem.block_map.offset == 72
+    assert L.Problem.block_heads.offset == 80 and ctypes.sizeof(L.Problem) == 88
 
 
 def problem(**kw):
@@ -74,6 +76,11 @@ def tens(**kw):
     (dict(sliding_window=-3), -1),
     (dict(soft_cap=-1.0), -1),
     (dict(scale=float("inf")), -1),
+    (dict(col_bounds=FAKE), -1),                              # column bounds without row bounds
+    (dict(doc_bounds=FAKE, seqlen_q=32), -4),                 # symmetric bounds need Sq == Skv
+    (dict(block_map=FAKE, block_heads=2), -1),                # block_heads not in {1, Hq}
+    (dict(block_map=FAKE, block_heads=1, seqlen_kv=2048 * 128 + 1), -6),  # block row longer than 2048
+    (dict(reserved=1), -1),
 ])
 def test_problem_rejections(kw, code):
     lib = L.load()
@@ -185,7 +192,7 @@ def test_integration_stub_matches_the_abi(monkeypatch):
         assert [f[0] for f in stub._fields_] == [f[0] for f in ours._fields_]
         for name, _ in ours._fields_:
             assert getattr(stub, name).offset == getattr(ours, name).offset, name
-    assert ctypes.sizeof(ns["FlexProblem"]) == 64 and ns["FlexProblem"].doc_bounds.offset == 56
+    assert ctypes.sizeof(ns["FlexProblem"]) == 88 and ns["FlexProblem"].block_map.offset == 72
 
 
 def test_header_struct_layout_compiled(tmp_path):
@@ -271,7 +278,9 @@ def test_bwd_workspace_range():
     assert ws(problem(head_dim=64)) == 0
     assert ws(problem(head_dim=256)) == 0
     assert ws(problem(head_dim=128, dtype=L.F32)) == 0
-    assert ws(problem(head_dim=128, doc_bounds=FAKE)) == 0
+    # masks keep the causal / window band of stored units (masked entries hold zeros)
+    assert ws(problem(head_dim=128, doc_bounds=FAKE)) == ws(problem(head_dim=128))
+    assert ws(problem(head_dim=128, block_map=FAKE, block_heads=1)) == ws(problem(head_dim=128))
     assert ws(problem(head_dim=128, heads_q=3)) == 0  # invalid problem
 
 

@@ -383,3 +383,101 @@ def test_row_chunked_group_with_window_skipping_columns():
             fin = torch.isfinite(y)
             assert torch.equal(torch.isfinite(x), fin)
             assert torch.allclose(x[fin], y[fin], atol=1e-12)
+
+
+# ------------------------------------------------ PrefixLM and block maps --
+def brute_forward_masked(q, k, v, causal, window, scale, prefix=None, keep=None):
+    """Scalar loops with the PrefixLM relaxation of the causal term (key j is
+    visible to every row when j < prefix[b]) and an arbitrary keep(b, h, i, j)
+    predicate (the block map), written as per-pair conditions."""
+    b, hq, sq, d = q.shape
+    hkv, skv = k.shape[1], k.shape[2]
+    g = hq // hkv
+    o = torch.zeros(b, hq, sq, d)
+    lse = torch.zeros(b, hq, sq)
+    for bi in range(b):
+        for h in range(hq):
+            for i in range(sq):
+                xs = []
+                for j in range(skv):
+                    if causal and j > i and not (prefix is not None and j < prefix[bi]):
+                        continue
+                    if window > 0 and i - j > window:
+                        continue
+                    if keep is not None and not keep(bi, h, i, j):
+                        continue
+                    x = scale * float(sum(q[bi, h, i, t] * k[bi, h // g, j, t] for t in range(d)))
+                    xs.append((j, x))
+                if not xs:
+                    lse[bi, h, i] = float("-inf")
+                    continue
+                mx = max(x for _, x in xs)
+                den = sum(math.exp(x - mx) for _, x in xs)
+                lse[bi, h, i] = mx + math.log(den)
+                for j, x in xs:
+                    o[bi, h, i] += math.exp(x - mx) / den * v[bi, h // g, j]
+    return o, lse
+
+
+def _close(o, lse, bo, blse):
+    assert torch.allclose(o, bo, atol=1e-12)
+    fin = torch.isfinite(blse)
+    assert torch.equal(torch.isfinite(lse), fin)
+    assert torch.allclose(lse[fin], blse[fin], atol=1e-12)
+
+
+@pytest.mark.parametrize("window", [0, 2])
+def test_prefix_lm_matches_brute_force(window):
+    q, k, v = rnd(2, 2, 9, 3, seed=11), rnd(2, 1, 9, 3, seed=12), rnd(2, 1, 9, 3, seed=13)
+    prefix = [3, 0]
+    o, lse = orc.forward(q, k, v, True, window, None, 0.6, 0.0, prefix_len=torch.tensor(prefix))
+    _close(o, lse, *brute_forward_masked(q, k, v, True, window, 0.6, prefix=prefix))
+
+
+def test_prefix_lm_special_cases():
+    q, k, v = rnd(1, 2, 10, 4, seed=14), rnd(1, 2, 10, 4, seed=15), rnd(1, 2, 10, 4, seed=16)
+    # prefix 0 is plain causal, a prefix covering every key is no mask at all
+    for pl, causal_ref in ((0, True), (10, False), (25, False)):
+        o, lse = orc.forward(q, k, v, True, 0, None, None, 0.0, prefix_len=torch.tensor([pl]))
+        ro, rl = orc.forward(q, k, v, causal_ref, 0, None, None, 0.0)
+        assert torch.equal(o, ro) and torch.equal(lse, rl)
+    # without causal the prefix changes nothing
+    o, _ = orc.forward(q, k, v, False, 0, None, None, 0.0, prefix_len=torch.tensor([4]))
+    assert torch.equal(o, orc.forward(q, k, v, False, 0, None, None, 0.0)[0])
+
+
+@pytest.mark.parametrize("causal,window", [(False, 0), (True, 0), (True, 3)])
+def test_block_map_matches_brute_force(causal, window):
+    q, k, v = rnd(1, 4, 11, 3, seed=17), rnd(1, 2, 9, 3, seed=18), rnd(1, 2, 9, 3, seed=19)
+    bs = 4  # tiny blocks: 3 x 3 map
+    gen = torch.Generator().manual_seed(5)
+    bm = (torch.rand(1, 4, 3, 3, generator=gen) > 0.4).to(torch.uint8)
+    bm[0, 1, 0] = 0  # a head whose first row block sees no key at all
+    o, lse = orc.forward(q, k, v, causal, window, None, 0.8, 0.0, block_map=bm, block_size=bs)
+    keep = lambda bi, h, i, j: bool(bm[bi, h, i // bs, j // bs])
+    _close(o, lse, *brute_forward_masked(q, k, v, causal, window, 0.8, keep=keep))
+    assert torch.isneginf(lse[0, 1, :4]).all() and (o[0, 1, :4] == 0).all()
+
+
+def test_block_map_special_cases():
+    q, k, v = rnd(1, 2, 300, 4, seed=20), rnd(1, 2, 300, 4, seed=21), rnd(1, 2, 300, 4, seed=22)
+    ones = torch.ones(1, 1, 3, 3, dtype=torch.uint8)
+    o, lse = orc.forward(q, k, v, True, 0, None, None, 0.0, block_map=ones)
+    ro, rl = orc.forward(q, k, v, True, 0, None, None, 0.0)
+    assert torch.equal(o, ro) and torch.equal(lse, rl)
+    # a block-diagonal map is a document mask with 128-aligned documents
+    diag = torch.eye(3, dtype=torch.uint8).view(1, 1, 3, 3)
+    ids = (torch.arange(300) // 128).view(1, -1)
+    o, lse = orc.forward(q, k, v, True, 0, None, None, 0.0, block_map=diag)
+    ro, rl = orc.forward(q, k, v, True, 0, None, None, 0.0, document_ids=ids)
+    assert torch.equal(o, ro) and torch.equal(lse, rl)
+
+
+def test_prefix_and_block_backward_closed_form_matches_autograd():
+    q, k, v, do = (rnd(1, 2, 8, 3, seed=s) for s in (23, 24, 25, 26))
+    bm = torch.tensor([[[[1, 0], [1, 1]]]], dtype=torch.uint8)
+    kw = dict(causal=True, sliding_window=0, scale=0.9, prefix_len=torch.tensor([3]), block_map=bm, block_size=4)
+    a = orc.backward(q, k, v, do, **kw)
+    b = orc.backward_autograd(q, k, v, do, **kw)
+    for x, y in zip(a, b):
+        assert torch.allclose(x, y, atol=1e-12)
