@@ -1,4 +1,4 @@
-// Flash-attention backward dQ from the staged dS (fp16/bf16, D = 128, gfx950).
+// Flash-attention backward dQ from the staged dS (fp16/bf16, D = 128 or 64, gfx950).
 //
 // Semantics: the dQ GEMM of npu_flash_attention.py:399 (dq += ds . k, ds
 // rounded to the input dtype before tl.dot), dQ = scale * dS K, with dS as
@@ -38,7 +38,7 @@
 
 namespace flexatt {
 
-#if FLEXATT_D == 128
+#if FLEXATT_D == 128 || FLEXATT_D == 64
 
 template <int D>
 struct DqsCfg {
@@ -66,7 +66,7 @@ void bwd_dq_ds_kernel(BwdArgs a) {
   using C = DqsCfg<D>;
   using M = Mfma<T>;
   using V8 = typename M::v8;
-  static_assert(D == 128 && C::KS == 4 && C::NSL == 4, "the MFMA blocking assumes D = 128, 64-row sub-blocks");
+  static_assert((D == 128 || D == 64) && C::KS == 4 && C::NSL == 4, "the MFMA blocking assumes D = 128 or 64, 64-row sub-blocks");
   __shared__ __attribute__((aligned(1024))) char smem[C::KSTAGES * C::KTILEB];
 
   const Shape& p = a.p;
@@ -220,10 +220,10 @@ void bwd_dq_ds_kernel(BwdArgs a) {
     const char* sK = smem + (i & (C::KSTAGES - 1)) * C::KTILEB;
     // 16 (k step, d-block) operand reads, each feeding one MFMA per slot
     i16x4 alo[3], ahi[3];
-    auto rdA = [&](int m, i16x4& lo, i16x4& hi) {
-      const int off = 16 * (m >> 2) * C::ROWB;
-      lo = lds_read_tr4(sK + (voff_lo[m & 3] + off));
-      hi = lds_read_tr4(sK + (voff_hi[m & 3] + off));
+    auto rdA = [&](int m, i16x4& lo, i16x4& hi) {  // k step m / DB, d-block m % DB
+      const int off = 16 * (m / C::DB) * C::ROWB;
+      lo = lds_read_tr4(sK + (voff_lo[m % C::DB] + off));
+      hi = lds_read_tr4(sK + (voff_hi[m % C::DB] + off));
     };
     rdA(0, alo[0], ahi[0]);
     rdA(1, alo[1], ahi[1]);
@@ -232,7 +232,7 @@ void bwd_dq_ds_kernel(BwdArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       if (m + 2 < C::KS * C::DB) rdA(m + 2, alo[(m + 2) % 3], ahi[(m + 2) % 3]);
       const V8 av = cat_tr<V8>(alo[m % 3], ahi[m % 3]);
-      const int ks = m >> 2, db = m & 3;
+      const int ks = m / C::DB, db = m % C::DB;
 #pragma unroll
       for (int c = 0; c < C::NSL; ++c)
         if (on[c]) acc[c][db] = M::mma(av, as_v8<V8>(cur[c * C::KS + ks]), acc[c][db]);
@@ -294,9 +294,14 @@ hipError_t launch_dq_ds(const BwdArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+#if FLEXATT_D == 128
 hipError_t bwd_dq_ds_bf16_d128(const BwdArgs& a, hipStream_t st) { return launch_dq_ds<__bf16, 128>(a, st); }
 hipError_t bwd_dq_ds_f16_d128(const BwdArgs& a, hipStream_t st) { return launch_dq_ds<_Float16, 128>(a, st); }
+#else
+hipError_t bwd_dq_ds_bf16_d64(const BwdArgs& a, hipStream_t st) { return launch_dq_ds<__bf16, 64>(a, st); }
+hipError_t bwd_dq_ds_f16_d64(const BwdArgs& a, hipStream_t st) { return launch_dq_ds<_Float16, 64>(a, st); }
+#endif
 
-#endif  // FLEXATT_D == 128
+#endif  // FLEXATT_D == 128 || FLEXATT_D == 64
 
 }  // namespace flexatt

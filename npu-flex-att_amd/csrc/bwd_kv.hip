@@ -55,7 +55,7 @@
 
 namespace flexatt {
 
-#if FLEXATT_D == 128
+#if FLEXATT_D == 128 || FLEXATT_D == 64
 
 template <int D>
 struct KvCfg {
@@ -70,7 +70,10 @@ struct KvCfg {
   static constexpr int TILEB = BM * ROWB;          // one of Q / dO
   static constexpr int E = TILEB / (1024 * NP);    // 1 KB copies per KV-wave per tensor
   static constexpr int STAGEB = 2 * TILEB + 2 * BM * 4;  // Q, dO, LSE, Delta
-  static constexpr int STAGES = 6;
+  // D = 64: five stages, so that two workgroups (74 KB of LDS each) share a
+  // CU at four waves per SIMD; D = 128: six stages, one workgroup per CU
+  static constexpr int STAGES = D == 64 ? 5 : 6;
+  static constexpr int WPE = D == 64 ? 4 : 2;      // waves per SIMD the register budget targets
   static constexpr int AHEAD = STAGES - 2;         // tile u + AHEAD is copied in step u
   static constexpr int XB = 4 * 64 * 16;           // packed P, P, dS, dS of one pair
   static constexpr int XOFF = STAGES * STAGEB;     // two exchange buffers
@@ -82,10 +85,17 @@ struct KvCfg {
 };
 
 template <class T, int D, bool SOFTCAP, bool ALIBI, bool DS>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(KvCfg<D>::WPE, KvCfg<D>::WPE)))
 void bwd_kv_kernel(BwdArgs a) {
   using C = KvCfg<D>;
-  static_assert(C::DB == 4 && C::KC == 8, "the hand-ordered phases assume D = 128");
+  static_assert((C::DB == 4 && C::KC == 8) || (C::DB == 2 && C::KC == 4), "the hand-ordered phases assume D = 128 or 64");
+  // S-wave: the LSE rows are read with MFMA LREAD of the phase and converted
+  // to log2 units over its last four MFMAs
+  constexpr int LREAD = C::KC == 8 ? 8 : 0, LCONV = 2 * C::KC - 4;
+  // KV-wave: transpose reads RAK MFMAs ahead (three at D = 64 without the
+  // soft-cap, where the 128-register budget is tightest for that wave;
+  // measured faster there, slower with the soft-cap)
+  constexpr int RAK = (D == 64 && !SOFTCAP) ? 3 : 4;
   using M = Mfma<T>;
   using V8 = typename M::v8;
   __shared__ __attribute__((aligned(1024))) char smem[C::LDSB];
@@ -211,12 +221,12 @@ void bwd_kv_kernel(BwdArgs a) {
         for (int k = 0; k < 2 * C::KC; ++k) {
           __builtin_amdgcn_sched_barrier(0);
           if (k + 4 < 2 * C::KC) ab[(k + 4) % 5] = rdA(k + 4);
-          if (k == 8) {  // query rows m0 + 8i + 4h + j
+          if (k == LREAD) {  // query rows m0 + 8i + 4h + j
 #pragma unroll
             for (int i = 0; i < 4; ++i) L4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 4 * h));
           }
-          if (k >= 12) {  // LSE -> log2 units
-            const int i = k - 12;
+          if (k >= LCONV) {  // LSE -> log2 units
+            const int i = k - LCONV;
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) L4[i][jj] *= kLog2e;
           }
@@ -427,7 +437,7 @@ void bwd_kv_kernel(BwdArgs a) {
       //      wave for tens of cycles at issue, so they stay out of the MFMA
       //      phase), packed P / dS of tile u-1, first transpose reads --------
       V8 PP[2], PS[2];
-      i16x4 blo[5], bhi[5];
+      i16x4 blo[RAK + 1], bhi[RAK + 1];
       if (ntile > 0) {
 #pragma unroll
         for (int j = 0; j < CNT; ++j) copy_op(s_cp, j);
@@ -452,7 +462,7 @@ void bwd_kv_kernel(BwdArgs a) {
           }
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) rdB(j, blo[j], bhi[j]);
+        for (int j = 0; j < RAK; ++j) rdB(j, blo[j], bhi[j]);
         if constexpr (DS) {
           // streamed past the caches: each fragment is read once, by the dQ kernel
 #pragma unroll
@@ -482,9 +492,9 @@ void bwd_kv_kernel(BwdArgs a) {
 #pragma unroll
         for (int j = 0; j < 4 * C::DB; ++j) {
           __builtin_amdgcn_sched_barrier(0);
-          if (j + 4 < 4 * C::DB) rdB(j + 4, blo[(j + 4) % 5], bhi[(j + 4) % 5]);
+          if (j + RAK < 4 * C::DB) rdB(j + RAK, blo[(j + RAK) % (RAK + 1)], bhi[(j + RAK) % (RAK + 1)]);
           const int db = (j >> 1) % C::DB, qc = (j >> 1) / C::DB;
-          const V8 av = cat_tr<V8>(blo[j % 5], bhi[j % 5]);
+          const V8 av = cat_tr<V8>(blo[j % (RAK + 1)], bhi[j % (RAK + 1)]);
           if (j & 1) dk[db] = M::mma(av, PS[qc], dk[db]);
           else dv[db] = M::mma(av, PP[qc], dv[db]);
         }
@@ -494,10 +504,12 @@ void bwd_kv_kernel(BwdArgs a) {
       if (ntile > 0) {
         advance();
         // tile u+1 landed.  Stores count in vmcnt too: with staged dS, the
-        // two stores of each step s >= 1 from step u-3 on (2 min(u, 4) of
-        // them) were issued after tile u+1's copies and may stay in flight.
+        // two stores of each step s >= 1 from step u + 1 - AHEAD on
+        // (2 min(u, AHEAD) of them) were issued after tile u+1's copies and
+        // may stay in flight.
         if constexpr (DS) {
-          if (u >= 4) wait_vmcnt<(C::AHEAD - 1) * CNT + 8>();
+          static_assert(C::AHEAD <= 4, "wait counts below cover AHEAD <= 4");
+          if (u >= C::AHEAD) wait_vmcnt<(C::AHEAD - 1) * CNT + 2 * C::AHEAD>();
           else if (u == 3) wait_vmcnt<(C::AHEAD - 1) * CNT + 6>();
           else if (u == 2) wait_vmcnt<(C::AHEAD - 1) * CNT + 4>();
           else if (u == 1) wait_vmcnt<(C::AHEAD - 1) * CNT + 2>();
@@ -546,11 +558,17 @@ hipError_t launch_kv(const BwdArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t bwd_kv_bf16_d128(const BwdArgs& a, hipStream_t st) { return launch_kv<__bf16, 128, false>(a, st); }
-hipError_t bwd_kv_f16_d128(const BwdArgs& a, hipStream_t st) { return launch_kv<_Float16, 128, false>(a, st); }
-hipError_t bwd_kv_ds_bf16_d128(const BwdArgs& a, hipStream_t st) { return launch_kv<__bf16, 128, true>(a, st); }
-hipError_t bwd_kv_ds_f16_d128(const BwdArgs& a, hipStream_t st) { return launch_kv<_Float16, 128, true>(a, st); }
+#define FLEXATT_KV_LAUNCHERS(D)                                                                     \
+  hipError_t bwd_kv_bf16_d##D(const BwdArgs& a, hipStream_t st) { return launch_kv<__bf16, D, false>(a, st); }    \
+  hipError_t bwd_kv_f16_d##D(const BwdArgs& a, hipStream_t st) { return launch_kv<_Float16, D, false>(a, st); }  \
+  hipError_t bwd_kv_ds_bf16_d##D(const BwdArgs& a, hipStream_t st) { return launch_kv<__bf16, D, true>(a, st); } \
+  hipError_t bwd_kv_ds_f16_d##D(const BwdArgs& a, hipStream_t st) { return launch_kv<_Float16, D, true>(a, st); }
+#if FLEXATT_D == 128
+FLEXATT_KV_LAUNCHERS(128)
+#else
+FLEXATT_KV_LAUNCHERS(64)
+#endif
 
-#endif  // FLEXATT_D == 128
+#endif  // FLEXATT_D == 128 || FLEXATT_D == 64
 
 }  // namespace flexatt

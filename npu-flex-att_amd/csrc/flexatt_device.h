@@ -179,15 +179,23 @@ __device__ __forceinline__ int swz_tr_inv(int r, int p) {
 // One layout for tiles that are read both ways: 16-byte row reads (rows as
 // MFMA operands; 16 lanes per LDS cycle read one chunk of 16 consecutive
 // rows) and transpose reads (32 lanes per LDS cycle read chunks 4j..4j+3 of
-// 4 consecutive rows 4i..4i+3).  Chunk c of row r sits at chunk c ^ g(r),
-// g(r) = (r mod 4) * 4 + (r / 4) mod 4: g is a permutation over any 16
-// consecutive rows (row reads hit 16 distinct bank groups) and 4 consecutive
-// rows differ in the top two bits of g (a transpose read's 16 chunks land in
-// 16 distinct bank groups).  The swizzle is its own inverse.
+// 4 consecutive rows 4i..4i+3).  The LDS serves 64 banks x 4 bytes, i.e. 16
+// groups of 16 bytes, per cycle.  Chunk c of row r sits at chunk c ^ g(r):
+//  * 256-byte rows (CPR 16, one row per bank row): g(r) = (r mod 4) * 4 +
+//    (r / 4) mod 4 is a permutation over any 16 consecutive rows (row reads
+//    hit 16 distinct groups) and 4 consecutive rows differ in the top two
+//    bits of g (a transpose read's 16 chunks land in 16 distinct groups);
+//  * 128-byte rows (CPR 8, rows 2i and 2i+1 share a bank row, group
+//    8 (r mod 2) + chunk): g(r) = 4 r1 + 2 r3 + r2 (r = r3 r2 r1 r0 in
+//    binary) is a permutation over the 8 rows of one parity in any aligned
+//    16 rows, and rows 4i, 4i+2 (and 4i+1, 4i+3) differ in bit 2 of g, so
+//    their 4-chunk groups fall in different halves of the bank row.
+// The swizzle is its own inverse.
 template <int CPR>
 __device__ __forceinline__ int swz_dual(int r, int c) {
-  static_assert(CPR == 16, "dual-use swizzle is defined for 256-byte rows");
-  return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
+  static_assert(CPR == 16 || CPR == 8, "dual-use swizzle is defined for 256- and 128-byte rows");
+  if constexpr (CPR == 16) return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
+  else return c ^ ((((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 1) | ((r >> 2) & 1));
 }
 template <int CPR>
 __device__ __forceinline__ int swz_dual_inv(int r, int p) {

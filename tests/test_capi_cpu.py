@@ -275,7 +275,8 @@ def test_bwd_workspace_range():
     ws = lib.flexatt_bwd_workspace
     assert ws(problem(head_dim=128)) > 0
     assert ws(problem(head_dim=128, dtype=L.F16)) > 0
-    assert ws(problem(head_dim=64)) == 0
+    assert ws(problem(head_dim=64)) == ws(problem(head_dim=128))  # 2 bytes per pair whatever D
+    assert ws(problem(head_dim=32)) == 0
     assert ws(problem(head_dim=256)) == 0
     assert ws(problem(head_dim=128, dtype=L.F32)) == 0
     # masks keep the causal / window band of stored units (masked entries hold zeros)
@@ -294,8 +295,8 @@ def test_staged_bwd_rejections():
     assert lib.flexatt_bwd_dkdv_ds(p, t, t, t, t, FAKE, FAKE, t, t, None, need, None) == -1
     assert lib.flexatt_bwd_dkdv_ds(p, t, t, t, t, FAKE, FAKE, t, t, FAKE + 8, need, None) == -5
     assert lib.flexatt_bwd_dq_ds(p, t, FAKE, need - 1, t, None) == -1
-    assert lib.flexatt_bwd_dq_ds(problem(head_dim=64), tens(), FAKE, need, tens(), None) == -6
-    assert lib.flexatt_bwd_dkdv_ds(problem(head_dim=64), tens(), tens(), tens(), tens(), FAKE, FAKE, tens(),
+    assert lib.flexatt_bwd_dq_ds(problem(head_dim=32), tens(), FAKE, need, tens(), None) == -6
+    assert lib.flexatt_bwd_dkdv_ds(problem(head_dim=32), tens(), tens(), tens(), tens(), FAKE, FAKE, tens(),
                                    tens(), FAKE, need, None) == -6
     assert lib.flexatt_bwd_ws(p, t, t, t, t, t, FAKE, FAKE, t, t, t, FAKE, need - 1, None) == -1
     assert lib.flexatt_bwd_ws(p, t, t, t, t, t, FAKE, FAKE, tens(stride_h=0, stride_s=128), t, t, FAKE, need,

@@ -1,6 +1,6 @@
 """GPU tests of the backward with dS staged through HBM (flexatt_bwd_ws: the
 dK/dV kernel writes its rounded dS, the dQ kernel streams dS K), the path
-npu_flash_attention_backward takes for fp16/bf16 with head_dim 128.
+npu_flash_attention_backward takes for fp16/bf16 with head_dim 128 or 64.
 
 * the five outputs against the float64 oracle at the north-star bounds, over
   GQA ratios 1, 2, 3, 4, 7 and 8 (head groups that do not fill a workgroup),
@@ -35,13 +35,21 @@ CASES = {
     "fp16_g2_one_key": (torch.float16, 1, 4, 2, 65, 1, {}),
     "bf16_g7_causal_sq_gt_skv": (torch.bfloat16, 1, 14, 2, 520, 130, dict(causal=True, scale=-0.08)),
     "fp16_g8_window_long": (torch.float16, 1, 8, 1, 1500, 1600, dict(sliding_window=513)),
+    # head_dim 64
+    "d64_bf16_g3_causal": (torch.bfloat16, 1, 6, 2, 300, 257, dict(causal=True, d=64)),
+    "d64_fp16_g7_all": (torch.float16, 1, 7, 1, 700, 650,
+                        dict(causal=True, sliding_window=200, alibi=True, soft_cap=30.0, scale=0.05, d=64)),
+    "d64_bf16_g1_full_sq_lt_skv": (torch.bfloat16, 2, 2, 2, 200, 333, dict(d=64)),
+    "d64_fp16_g4_window": (torch.float16, 1, 8, 2, 1000, 1000, dict(sliding_window=300, d=64)),
+    "d64_fp16_g2_one_key": (torch.float16, 1, 4, 2, 65, 1, dict(d=64)),
 }
 
 
 def _inputs(case, seed=0):
     dtype, b, hq, hkv, sq, skv, kw = CASES[case]
     kw = dict(kw)
-    cpu, dev = draw(seed + 90, b, hq, hkv, sq, skv, 128, dtype)
+    d = kw.pop("d", 128)
+    cpu, dev = draw(seed + 90, b, hq, hkv, sq, skv, d, dtype)
     if kw.pop("alibi", False):
         kw["alibi_slope"] = alibi_slopes(hq).to("cuda")
     return dtype, cpu, dev, kw
@@ -63,7 +71,8 @@ def test_staged_matches_oracle(gpu_device, case):
         check(name, x, r, dtype)
 
 
-@pytest.mark.parametrize("case", ["bf16_g3_causal", "fp16_g1_window_alibi_cap", "bf16_g7_causal_sq_gt_skv"])
+@pytest.mark.parametrize("case", ["bf16_g3_causal", "fp16_g1_window_alibi_cap", "bf16_g7_causal_sq_gt_skv",
+                                  "d64_fp16_g7_all"])
 def test_staged_ds_values(gpu_device, case):
     """Decode the workspace: unit (b, h, t, kb) fragment f, lane l, element e
     holds dS/scale of query row 32 t + l % 32 and KV row
@@ -114,7 +123,7 @@ def test_staged_ds_values(gpu_device, case):
     assert e <= tol, f"staged dS err {e:.3e} > {tol}"
 
 
-@pytest.mark.parametrize("case", ["bf16_g8_causal_window", "fp16_g7_full_sq_lt_skv", "bf16_g4_all"])
+@pytest.mark.parametrize("case", ["bf16_g8_causal_window", "fp16_g7_full_sq_lt_skv", "bf16_g4_all", "d64_fp16_g4_window"])
 def test_staged_against_recompute_path(gpu_device, case):
     dtype, cpu, (q, k, v, do), kw = _inputs(case)
     o, lse = nfa.npu_flash_attention_forward(q, k, v, return_lse=True, **kw)
@@ -132,7 +141,7 @@ def test_staged_against_recompute_path(gpu_device, case):
         check(name, x, r.double(), dtype)
 
 
-@pytest.mark.parametrize("case", ["bf16_g3_causal", "fp16_g1_window_alibi_cap"])
+@pytest.mark.parametrize("case", ["bf16_g3_causal", "fp16_g1_window_alibi_cap", "d64_bf16_g3_causal"])
 def test_staged_kernels_and_repeats_bitwise(gpu_device, case):
     dtype, cpu, (q, k, v, do), kw = _inputs(case)
     lib = L.load()
@@ -175,11 +184,12 @@ def test_staged_kernels_and_repeats_bitwise(gpu_device, case):
     assert torch.equal(c[1], c[4]) and torch.equal(c[2], c[5]), "staging changed dK/dV"
 
 
+@pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
-def test_staged_fully_masked_rows(gpu_device, dtype):
+def test_staged_fully_masked_rows(gpu_device, dtype, d):
     """Non-causal window W = 30 over Skv = 100 keys: query rows >= 131 see
     none (O = 0, LSE = -inf) and get dQ = 0; the others match the oracle."""
-    cpu, (q, k, v, do) = draw(5, 1, 4, 2, 400, 100, 128, dtype)
+    cpu, (q, k, v, do) = draw(5, 1, 4, 2, 400, 100, d, dtype)
     kw = dict(sliding_window=30)
     o, lse, dq, dk, dv = fwd_bwd(nfa, q, k, v, do, **kw)
     ref = oracle_fwd_bwd(*cpu, **kw)
