@@ -176,7 +176,7 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
                 const float* lse, float* delta, const flexatt_tensor* dq, const flexatt_tensor* dk,
                 const flexatt_tensor* dv, void* stream);
 
-/* Backward with dS staged through HBM (fp16/bf16, head_dim 64 or 128).  The dK/dV kernel already forms dS for every attended
+/* Backward with dS staged through HBM (fp16/bf16, head_dim 64, 128 or 256).  The dK/dV kernel already forms dS for every attended
  * pair; it writes those values (rounded to the input dtype, as its own dK
  * MFMAs consume them) to a caller-owned workspace, and the dQ kernel forms
  * dQ = scale * dS K from them instead of recomputing S and dP.  The

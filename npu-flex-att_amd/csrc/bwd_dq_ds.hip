@@ -1,4 +1,4 @@
-// Flash-attention backward dQ from the staged dS (fp16/bf16, D = 128 or 64, gfx950).
+// Flash-attention backward dQ from the staged dS (fp16/bf16, D = 64, 128 or 256, gfx950).
 //
 // Semantics: the dQ GEMM of npu_flash_attention.py:399 (dq += ds . k, ds
 // rounded to the input dtype before tl.dot), dQ = scale * dS K, with dS as
@@ -10,10 +10,10 @@
 //
 // Decomposition
 //  * A workgroup is 4 waves, one per SIMD, for one (b, KV head) and 16 query
-//    slots (a slot is 32 rows of one query head): nh heads (4, 2 or 1, the
-//    largest dividing Hq / Hkv) x 16 / nh query tiles.  Wave v owns slots
-//    4v .. 4v + 3, all inside one aligned group of four query tiles, lane =
-//    query row; its dQ^T (4 slots x 128 x 32 fp32) lives in the accumulation
+//    slots (8 at D = 256; a slot is 32 rows of one query head): nh heads (4,
+//    2 or 1, the largest dividing Hq / Hkv) x slots / nh query tiles.  Wave v
+//    owns slots NSL v .. NSL v + NSL - 1 (NSL = 4, or 2 at D = 256), lane =
+//    query row; its dQ^T (NSL slots x D x 32 fp32) lives in the accumulation
 //    registers.
 //  * The workgroup walks the 64-row KV sub-blocks its slots' dS bands cover.
 //    K rows (16 KB per sub-block, read by all waves) go global -> LDS with
@@ -38,12 +38,13 @@
 
 namespace flexatt {
 
-#if FLEXATT_D == 128 || FLEXATT_D == 64
+#if FLEXATT_D == 128 || FLEXATT_D == 64 || FLEXATT_D == 256
 
 template <int D>
 struct DqsCfg {
   static constexpr int NW = 4;                 // waves per workgroup, one per SIMD
-  static constexpr int NSL = 4;                // query slots per wave
+  static constexpr int NSL = D == 256 ? 2 : 4;  // query slots per wave (256 accumulator registers at D = 256)
+  static constexpr int SLOTS = NW * NSL;        // query slots per workgroup
   static constexpr int SB = 64;                // KV rows per sub-block
   static constexpr int KS = SB / 16;           // k steps per sub-block
   static constexpr int DB = D / 32;            // d-blocks of dQ^T
@@ -57,7 +58,7 @@ struct DqsCfg {
   static constexpr int DAHEAD = 2;             // dS loads run this many sub-blocks ahead
   static constexpr int NDS = NSL * KS;         // dS operands (1 KB loads) per sub-block
   static_assert(EK * 1024 * NW == KTILEB && SUBB == KS * 1024, "1 KB pieces");
-  static_assert(KSTAGES * KTILEB <= 64 * 1024, "LDS");
+  static_assert(KSTAGES * KTILEB <= 128 * 1024, "LDS");
 };
 
 template <class T, int D>
@@ -66,7 +67,7 @@ void bwd_dq_ds_kernel(BwdArgs a) {
   using C = DqsCfg<D>;
   using M = Mfma<T>;
   using V8 = typename M::v8;
-  static_assert((D == 128 || D == 64) && C::KS == 4 && C::NSL == 4, "the MFMA blocking assumes D = 128 or 64, 64-row sub-blocks");
+  static_assert((D == 64 || D == 128 || D == 256) && C::KS == 4, "the MFMA blocking assumes 64-row sub-blocks");
   __shared__ __attribute__((aligned(1024))) char smem[C::KSTAGES * C::KTILEB];
 
   const Shape& p = a.p;
@@ -76,10 +77,10 @@ void bwd_dq_ds_kernel(BwdArgs a) {
 
   // Work item: (b, hkv, head group, query block), the query blocks of one
   // (b, hkv) consecutive (they share K in one XCD's L2), longest causal
-  // bands first.  A block holds 16 slots: nh heads x (16 / nh) query tiles.
+  // bands first.  A block holds SLOTS slots: nh heads x (SLOTS / nh) query tiles.
   const int nh = a.ntiles & 0xff;  // heads per workgroup: 4, 2 or 1 (divides G)
   const int nqb = a.ntiles >> 8;   // query blocks per head group
-  const int nq = 16 / nh;          // query tiles per block
+  const int nq = C::SLOTS / nh;    // query tiles per block
   const int w = xcd_remap(blockIdx.x, gridDim.x);
   const int qb = nqb - 1 - (w % nqb);
   int rest = w / nqb;
@@ -172,8 +173,10 @@ void bwd_dq_ds_kernel(BwdArgs a) {
   };
   auto wait_ds = [&](i32x4 (&buf)[C::NDS], auto n_c) {
     constexpr int N = decltype(n_c)::value;
+    static_assert(C::NDS == 8 || C::NDS == 16, "dS operand count");
     wait_vmcnt_tied<N>(buf[0], buf[1], buf[2], buf[3], buf[4], buf[5], buf[6], buf[7]);
-    wait_vmcnt_tied<N>(buf[8], buf[9], buf[10], buf[11], buf[12], buf[13], buf[14], buf[15]);
+    if constexpr (C::NDS == 16)
+      wait_vmcnt_tied<N>(buf[8], buf[9], buf[10], buf[11], buf[12], buf[13], buf[14], buf[15]);
   };
 
   // Transpose-read offsets (A operands K^T: rows 4h + (lane % 16) / 4 and
@@ -285,7 +288,7 @@ hipError_t launch_dq_ds(const BwdArgs& a, hipStream_t st) {
   using C = DqsCfg<D>;
   BwdArgs x = a;
   const int nh = (a.p.G % 4 == 0) ? 4 : (a.p.G % 2 == 0) ? 2 : 1;
-  const int nq = 16 / nh;
+  const int nq = C::SLOTS / nh;
   const int nqt = (a.p.Sq + kDsQT - 1) / kDsQT;
   const int nqb = (nqt + nq - 1) / nq;
   x.ntiles = (nqb << 8) | nh;
@@ -294,14 +297,17 @@ hipError_t launch_dq_ds(const BwdArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+#define FLEXATT_DQ_DS_LAUNCHERS(D)                                                                     \
+  hipError_t bwd_dq_ds_bf16_d##D(const BwdArgs& a, hipStream_t st) { return launch_dq_ds<__bf16, D>(a, st); } \
+  hipError_t bwd_dq_ds_f16_d##D(const BwdArgs& a, hipStream_t st) { return launch_dq_ds<_Float16, D>(a, st); }
 #if FLEXATT_D == 128
-hipError_t bwd_dq_ds_bf16_d128(const BwdArgs& a, hipStream_t st) { return launch_dq_ds<__bf16, 128>(a, st); }
-hipError_t bwd_dq_ds_f16_d128(const BwdArgs& a, hipStream_t st) { return launch_dq_ds<_Float16, 128>(a, st); }
+FLEXATT_DQ_DS_LAUNCHERS(128)
+#elif FLEXATT_D == 64
+FLEXATT_DQ_DS_LAUNCHERS(64)
 #else
-hipError_t bwd_dq_ds_bf16_d64(const BwdArgs& a, hipStream_t st) { return launch_dq_ds<__bf16, 64>(a, st); }
-hipError_t bwd_dq_ds_f16_d64(const BwdArgs& a, hipStream_t st) { return launch_dq_ds<_Float16, 64>(a, st); }
+FLEXATT_DQ_DS_LAUNCHERS(256)
 #endif
 
-#endif  // FLEXATT_D == 128 || FLEXATT_D == 64
+#endif  // FLEXATT_D == 128 || FLEXATT_D == 64 || FLEXATT_D == 256
 
 }  // namespace flexatt

@@ -55,7 +55,7 @@
 
 namespace flexatt {
 
-#if FLEXATT_D == 128 || FLEXATT_D == 64
+#if FLEXATT_D == 128 || FLEXATT_D == 64 || FLEXATT_D == 256
 
 template <int D>
 struct KvCfg {
@@ -71,11 +71,17 @@ struct KvCfg {
   static constexpr int E = TILEB / (1024 * NP);    // 1 KB copies per KV-wave per tensor
   static constexpr int STAGEB = 2 * TILEB + 2 * BM * 4;  // Q, dO, LSE, Delta
   // D = 64: five stages, so that two workgroups (74 KB of LDS each) share a
-  // CU at four waves per SIMD; D = 128: six stages, one workgroup per CU
-  static constexpr int STAGES = D == 64 ? 5 : 6;
+  // CU at four waves per SIMD; D = 128: six stages, one workgroup per CU;
+  // D = 256: four (32 KB each)
+  static constexpr int STAGES = D == 64 ? 5 : (D == 128 ? 6 : 4);
   static constexpr int WPE = D == 64 ? 4 : 2;      // waves per SIMD the register budget targets
   static constexpr int AHEAD = STAGES - 2;         // tile u + AHEAD is copied in step u
-  static constexpr int XB = 4 * 64 * 16;           // packed P, P, dS, dS of one pair
+  // D = 256 runs dV and dK in two passes (two launches), so that the KV-wave
+  // holds one 128-register accumulator set; each pass exchanges one packed
+  // operand (P, or dS) instead of both
+  static constexpr bool PASSES = D == 256;
+  static constexpr int XSLOTS = PASSES ? 2 : 4;    // 1 KB slots per pair: P, P, dS, dS (or P, P / dS, dS)
+  static constexpr int XB = XSLOTS * 64 * 16;
   static constexpr int XOFF = STAGES * STAGEB;     // two exchange buffers
   static constexpr int LDSB = XOFF + 2 * NP * XB;
   static constexpr int RPW = BM / NP;              // LSE / Delta rows copied per KV-wave
@@ -84,14 +90,22 @@ struct KvCfg {
   static_assert(STAGEB % 256 == 0 && LDSB <= 160 * 1024, "LDS layout");
 };
 
-template <class T, int D, bool SOFTCAP, bool ALIBI, bool DS>
+// PASS 0: dV and dK together; PASS 1: dV only; PASS 2: dK only (with the
+// staged dS when DS).
+template <class T, int D, bool SOFTCAP, bool ALIBI, bool DS, int PASS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(KvCfg<D>::WPE, KvCfg<D>::WPE)))
 void bwd_kv_kernel(BwdArgs a) {
   using C = KvCfg<D>;
-  static_assert((C::DB == 4 && C::KC == 8) || (C::DB == 2 && C::KC == 4), "the hand-ordered phases assume D = 128 or 64");
+  static_assert(C::DB == 2 * C::KC / 4 && (D == 64 || D == 128 || D == 256), "head dims 64, 128, 256");
+  static_assert((PASS == 0) != C::PASSES && !(DS && PASS == 1), "passes: D = 256 only; dS staged by the dK pass");
+  constexpr bool DOV = PASS != 2, DOK = PASS != 1;  // accumulate dV / dK
+  // S-wave MFMAs per tile: S (and, for dK, dP)
+  constexpr int NM = DOK ? 2 * C::KC : C::KC;
   // S-wave: the LSE rows are read with MFMA LREAD of the phase and converted
   // to log2 units over its last four MFMAs
-  constexpr int LREAD = C::KC == 8 ? 8 : 0, LCONV = 2 * C::KC - 4;
+  constexpr int LREAD = NM >= 16 ? 8 : 0, LCONV = NM - 4;
+  // exchange slots of P and dS
+  constexpr int SLOT_P = 0, SLOT_DS = C::XSLOTS == 4 ? 2 : 0;
   // KV-wave: transpose reads RAK MFMAs ahead (three at D = 64 without the
   // soft-cap, where the 128-register budget is tightest for that wave;
   // measured faster there, slower with the soft-cap)
@@ -145,8 +159,8 @@ void bwd_kv_kernel(BwdArgs a) {
       voff_hi[db] = (tr_row + 8) * C::ROWB + swz_dual<C::CPR>(tr_row + 8, c) * 16 + e2;
     }
   }
-  // This lane's 16-byte slot of packed operand i (0, 1: P; 2, 3: dS) in the
-  // exchange buffer of tile u.
+  // This lane's 16-byte slot of packed operand i (SLOT_P, + 1: P; SLOT_DS,
+  // + 1: dS) in the exchange buffer of tile u.
   auto xslot = [&](int u, int i) {
     return smem + C::XOFF + (u & 1) * (C::NP * C::XB) + pr * C::XB + i * 1024 + lane * 16;
   };
@@ -162,8 +176,9 @@ void bwd_kv_kernel(BwdArgs a) {
       for (int kc = 0; kc < C::KC; ++kc) {
         kreg[kc] = as_v8<V8>(ld_global16(kr + 16 * kc));
         // -V: the dP MFMAs start from Delta and so end at Delta - dP (below)
-        vreg[kc] = as_v8<V8>(ld_global16(vr + 16 * kc) ^ i32x4{(int)0x80008000, (int)0x80008000,
-                                                                (int)0x80008000, (int)0x80008000});
+        if constexpr (DOK)
+          vreg[kc] = as_v8<V8>(ld_global16(vr + 16 * kc) ^ i32x4{(int)0x80008000, (int)0x80008000,
+                                                                  (int)0x80008000, (int)0x80008000});
       }
     }
     constexpr bool RAW = !SOFTCAP && !ALIBI;
@@ -203,24 +218,31 @@ void bwd_kv_kernel(BwdArgs a) {
         int ra[C::KC];
 #pragma unroll
         for (int kc = 0; kc < C::KC; ++kc) ra[kc] = rowoff[kc] + sc * C::STAGEB;
-        auto rdA = [&](int k) { return lds_read16(smem + (ra[k >> 1] + (k & 1) * C::TILEB)); };
-        // Delta of the query rows m0 + 8i + 4h + j is the initial dP
-        // accumulator (element 4i + j), so that P (dP - Delta) needs no
-        // subtraction on the VALU.
+        // MFMA k reads Q row chunk k (S only) or, interleaving S and dP,
+        // chunk k / 2 of Q (even k) or dO (odd k)
+        auto rdA = [&](int k) {
+          if constexpr (DOK) return lds_read16(smem + (ra[k >> 1] + (k & 1) * C::TILEB));
+          else return lds_read16(smem + ra[k]);
+        };
         const float* sR = (const float*)(smem + sc * C::STAGEB + 2 * C::TILEB);
-        f32x4 D4[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) D4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 8 + 4 * h));
         i32x4 ab[5];
+        S = f32x16{};
+        if constexpr (DOK) {
+          // Delta of the query rows m0 + 8i + 4h + j is the initial dP
+          // accumulator (element 4i + j), so that P (dP - Delta) needs no
+          // subtraction on the VALU.
+          f32x4 D4[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) D4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 8 + 4 * h));
+          DP = f32x16{D4[0][0], D4[0][1], D4[0][2], D4[0][3], D4[1][0], D4[1][1], D4[1][2], D4[1][3],
+                      D4[2][0], D4[2][1], D4[2][2], D4[2][3], D4[3][0], D4[3][1], D4[3][2], D4[3][3]};
+        }
 #pragma unroll
         for (int k = 0; k < 4; ++k) ab[k] = rdA(k);
-        S = f32x16{};
-        DP = f32x16{D4[0][0], D4[0][1], D4[0][2], D4[0][3], D4[1][0], D4[1][1], D4[1][2], D4[1][3],
-                    D4[2][0], D4[2][1], D4[2][2], D4[2][3], D4[3][0], D4[3][1], D4[3][2], D4[3][3]};
 #pragma unroll
-        for (int k = 0; k < 2 * C::KC; ++k) {
+        for (int k = 0; k < NM; ++k) {
           __builtin_amdgcn_sched_barrier(0);
-          if (k + 4 < 2 * C::KC) ab[(k + 4) % 5] = rdA(k + 4);
+          if (k + 4 < NM) ab[(k + 4) % 5] = rdA(k + 4);
           if (k == LREAD) {  // query rows m0 + 8i + 4h + j
 #pragma unroll
             for (int i = 0; i < 4; ++i) L4[i] = __builtin_bit_cast(f32x4, lds_read16(sR + 16 * i + 4 * h));
@@ -230,12 +252,13 @@ void bwd_kv_kernel(BwdArgs a) {
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) L4[i][jj] *= kLog2e;
           }
-          if (k & 1) DP = M::mma(as_v8<V8>(ab[k % 5]), vreg[k >> 1], DP);
+          if constexpr (!DOK) S = M::mma(as_v8<V8>(ab[k % 5]), kreg[k], S);
+          else if (k & 1) DP = M::mma(as_v8<V8>(ab[k % 5]), vreg[k >> 1], DP);
           else S = M::mma(as_v8<V8>(ab[k % 5]), kreg[k >> 1], S);
         }
         __builtin_amdgcn_sched_barrier(0);
         pin(S);
-        pin(DP);
+        if constexpr (DOK) pin(DP);
       }
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();  // X(u)
@@ -279,17 +302,23 @@ void bwd_kv_kernel(BwdArgs a) {
             pe[r] = e;
           }
           __builtin_amdgcn_sched_barrier(0);
+          if constexpr (DOK) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float ds = -pe[r] * DP[r];  // P (dP - Delta)
-            if constexpr (SOFTCAP) ds *= 1.f - tt[r] * tt[r];
-            de[r] = ds;
+            for (int r = 0; r < 16; ++r) {
+              float ds = -pe[r] * DP[r];  // P (dP - Delta)
+              if constexpr (SOFTCAP) ds *= 1.f - tt[r] * tt[r];
+              de[r] = ds;
+            }
           }
           __builtin_amdgcn_sched_barrier(0);
-          *(V8*)xslot(u, 0) = pack8<T>(pe, 0);
-          *(V8*)xslot(u, 1) = pack8<T>(pe, 8);
-          *(V8*)xslot(u, 2) = pack8<T>(de, 0);
-          *(V8*)xslot(u, 3) = pack8<T>(de, 8);
+          if constexpr (DOV) {
+            *(V8*)xslot(u, SLOT_P) = pack8<T>(pe, 0);
+            *(V8*)xslot(u, SLOT_P + 1) = pack8<T>(pe, 8);
+          }
+          if constexpr (DOK) {
+            *(V8*)xslot(u, SLOT_DS) = pack8<T>(de, 0);
+            *(V8*)xslot(u, SLOT_DS + 1) = pack8<T>(de, 8);
+          }
         };
         if ((m0 + C::BM > p.Sq) || kv_tail || (p.causal && m0 < kw0 + 31) ||
             (p.window > 0 && m0 + C::BM - 1 - kw0 > p.window) || m0 < pc_lo || m0 + C::BM > pc_hi || !live)
@@ -391,9 +420,25 @@ void bwd_kv_kernel(BwdArgs a) {
     // are the lane addresses in the tile's stage (Q / dO and the 16-row block
     // fold into the instruction offset).
     int tb_lo[C::DB], tb_hi[C::DB];
+    // MFMA j: d-block db, query half qc, dK (Q^T, dS) or dV (dO^T, P); both
+    // interleaved (PASS 0) or one of them
+    constexpr int NJ = (PASS == 0 ? 4 : 2) * C::DB;
+    auto jmap = [&](int j, int& db, int& qc, bool& isk) {
+      if constexpr (PASS == 0) {
+        db = (j >> 1) % C::DB;
+        qc = (j >> 1) / C::DB;
+        isk = j & 1;
+      } else {
+        db = j % C::DB;
+        qc = j / C::DB;
+        isk = PASS == 2;
+      }
+    };
     auto rdB = [&](int j, i16x4& lo, i16x4& hi) {
-      const int db = (j >> 1) % C::DB, qc = (j >> 1) / C::DB;
-      const int off = ((j & 1) ? 0 : C::TILEB) + 16 * qc * C::ROWB;
+      int db, qc;
+      bool isk;
+      jmap(j, db, qc, isk);
+      const int off = (isk ? 0 : C::TILEB) + 16 * qc * C::ROWB;
       lo = lds_read_tr4(smem + (tb_lo[db] + off));
       hi = lds_read_tr4(smem + (tb_hi[db] + off));
     };
@@ -415,7 +460,7 @@ void bwd_kv_kernel(BwdArgs a) {
     if constexpr (DS) {
       const int aq = 4 * ((lane >> 4) & 1) + (lane & 3);
       const int jr = 4 * (lane >> 5) + ((lane & 15) >> 2);
-      xtr = C::XOFF + pr * C::XB + (2 + (aq >> 2)) * 1024 + (((aq & 1) << 5) + jr) * 16 + 8 * ((aq >> 1) & 1);
+      xtr = C::XOFF + pr * C::XB + (SLOT_DS + (aq >> 2)) * 1024 + (((aq & 1) << 5) + jr) * 16 + 8 * ((aq >> 1) & 1);
       const int64_t unit = (int64_t)(b * p.Hq + hk * p.G) * a.ds_head +
                            ds_tile_offset(qt_top, p.causal, p.window, nkb) + kb - ds_kb_lo(qt_top, p.window, nkb);
       dsp = a.ds + unit * kDsUnitB + (2 * pr) * 1024 + lane * 16;
@@ -448,10 +493,14 @@ void bwd_kv_kernel(BwdArgs a) {
           tb_lo[db] = voff_lo[db] + s_tr * C::STAGEB;
           tb_hi[db] = voff_hi[db] + s_tr * C::STAGEB;
         }
-        PP[0] = *(const V8*)xslot(u - 1, 0);
-        PP[1] = *(const V8*)xslot(u - 1, 1);
-        PS[0] = *(const V8*)xslot(u - 1, 2);
-        PS[1] = *(const V8*)xslot(u - 1, 3);
+        if constexpr (DOV) {
+          PP[0] = *(const V8*)xslot(u - 1, SLOT_P);
+          PP[1] = *(const V8*)xslot(u - 1, SLOT_P + 1);
+        }
+        if constexpr (DOK) {
+          PS[0] = *(const V8*)xslot(u - 1, SLOT_DS);
+          PS[1] = *(const V8*)xslot(u - 1, SLOT_DS + 1);
+        }
         i16x4 st4[4];
         if constexpr (DS) {
           const char* xb = smem + xtr + ((u - 1) & 1) * (C::NP * C::XB);
@@ -490,12 +539,14 @@ void bwd_kv_kernel(BwdArgs a) {
       // ---- V(u): dV / dK of tile u-1 ---------------------------------------
       if (act) {
 #pragma unroll
-        for (int j = 0; j < 4 * C::DB; ++j) {
+        for (int j = 0; j < NJ; ++j) {
           __builtin_amdgcn_sched_barrier(0);
-          if (j + RAK < 4 * C::DB) rdB(j + RAK, blo[(j + RAK) % (RAK + 1)], bhi[(j + RAK) % (RAK + 1)]);
-          const int db = (j >> 1) % C::DB, qc = (j >> 1) / C::DB;
+          if (j + RAK < NJ) rdB(j + RAK, blo[(j + RAK) % (RAK + 1)], bhi[(j + RAK) % (RAK + 1)]);
+          int db, qc;
+          bool isk;
+          jmap(j, db, qc, isk);
           const V8 av = cat_tr<V8>(blo[j % (RAK + 1)], bhi[j % (RAK + 1)]);
-          if (j & 1) dk[db] = M::mma(av, PS[qc], dk[db]);
+          if (isk) dk[db] = M::mma(av, PS[qc], dk[db]);
           else dv[db] = M::mma(av, PP[qc], dv[db]);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -534,10 +585,12 @@ void bwd_kv_kernel(BwdArgs a) {
       for (int db = 0; db < C::DB; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          st_global8(kq + 32 * db + 8 * i, pack4<T>(dk[db][4 * i] * sc, dk[db][4 * i + 1] * sc,
-                                                   dk[db][4 * i + 2] * sc, dk[db][4 * i + 3] * sc));
-          st_global8(vq + 32 * db + 8 * i, pack4<T>(dv[db][4 * i], dv[db][4 * i + 1], dv[db][4 * i + 2],
-                                                   dv[db][4 * i + 3]));
+          if constexpr (DOK)
+            st_global8(kq + 32 * db + 8 * i, pack4<T>(dk[db][4 * i] * sc, dk[db][4 * i + 1] * sc,
+                                                     dk[db][4 * i + 2] * sc, dk[db][4 * i + 3] * sc));
+          if constexpr (DOV)
+            st_global8(vq + 32 * db + 8 * i, pack4<T>(dv[db][4 * i], dv[db][4 * i + 1], dv[db][4 * i + 2],
+                                                     dv[db][4 * i + 3]));
         }
     }
   }
@@ -551,11 +604,22 @@ hipError_t launch_kv(const BwdArgs& a, hipStream_t st) {
   x.ntiles = (a.p.Skv + C::BKV - 1) / C::BKV;
   const dim3 grid(x.ntiles * a.p.B * a.p.Hkv), block(C::NW * 64);
   const bool sc = a.p.cap > 0.f, al = a.p.alibi != nullptr;
-  if (sc && al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, true, DS>), grid, block, 0, st, x);
-  else if (sc) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, false, DS>), grid, block, 0, st, x);
-  else if (al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, true, DS>), grid, block, 0, st, x);
-  else hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, false, DS>), grid, block, 0, st, x);
-  return hipGetLastError();
+  auto go = [&](auto pass_c) {
+    constexpr int PS = decltype(pass_c)::value;
+    constexpr bool DSP = DS && PS != 1;
+    if (sc && al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, true, DSP, PS>), grid, block, 0, st, x);
+    else if (sc) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, false, DSP, PS>), grid, block, 0, st, x);
+    else if (al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, true, DSP, PS>), grid, block, 0, st, x);
+    else hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, false, DSP, PS>), grid, block, 0, st, x);
+    return hipGetLastError();
+  };
+  if constexpr (C::PASSES) {
+    const hipError_t e = go(std::integral_constant<int, 1>{});
+    if (e != hipSuccess) return e;
+    return go(std::integral_constant<int, 2>{});
+  } else {
+    return go(std::integral_constant<int, 0>{});
+  }
 }
 
 #define FLEXATT_KV_LAUNCHERS(D)                                                                     \
@@ -565,10 +629,12 @@ hipError_t launch_kv(const BwdArgs& a, hipStream_t st) {
   hipError_t bwd_kv_ds_f16_d##D(const BwdArgs& a, hipStream_t st) { return launch_kv<_Float16, D, true>(a, st); }
 #if FLEXATT_D == 128
 FLEXATT_KV_LAUNCHERS(128)
-#else
+#elif FLEXATT_D == 64
 FLEXATT_KV_LAUNCHERS(64)
+#else
+FLEXATT_KV_LAUNCHERS(256)
 #endif
 
-#endif  // FLEXATT_D == 128 || FLEXATT_D == 64
+#endif  // FLEXATT_D == 128 || FLEXATT_D == 64 || FLEXATT_D == 256
 
 }  // namespace flexatt

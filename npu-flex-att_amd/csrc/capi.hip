@@ -139,8 +139,8 @@ const BwdLauncher kDq[3][4] = {
 };
 const BwdLauncher kDkdv[3][4] = {
     {bwd_dkdv_simt_f32_d32, bwd_dkdv_simt_f32_d64, bwd_dkdv_simt_f32_d128, bwd_dkdv_simt_f32_d256},
-    {bwd_dkdv_mfma_f16_d32, bwd_kv_f16_d64, bwd_kv_f16_d128, bwd_dkdv_mfma_f16_d256},
-    {bwd_dkdv_mfma_bf16_d32, bwd_kv_bf16_d64, bwd_kv_bf16_d128, bwd_dkdv_mfma_bf16_d256},
+    {bwd_dkdv_mfma_f16_d32, bwd_kv_f16_d64, bwd_kv_f16_d128, bwd_kv_f16_d256},
+    {bwd_dkdv_mfma_bf16_d32, bwd_kv_bf16_d64, bwd_kv_bf16_d128, bwd_kv_bf16_d256},
 };
 
 // Split-KV decode: range, plan and workspace.
@@ -279,20 +279,25 @@ int bwd_common(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_
   return FLEXATT_OK;
 }
 
-// Staged dS (D = 128 and 64, fp16/bf16, every mask primitive: the dK/dV
-// kernel masks per element and stores every unit of the causal / window
-// band, zero where masked): units per query head and workspace bytes; 0
-// when the problem takes the recomputing dQ kernel.
+// Staged dS (D = 64, 128 and 256, fp16/bf16, every mask primitive: the
+// dK/dV kernel masks per element and stores every unit of the causal /
+// window band, zero where masked): units per query head and workspace
+// bytes; 0 when the problem takes the recomputing dQ kernel.
 bool ds_applies(const flexatt_problem* p) {
-  return (p->dtype == FLEXATT_F16 || p->dtype == FLEXATT_BF16) && (p->head_dim == 128 || p->head_dim == 64);
+  return (p->dtype == FLEXATT_F16 || p->dtype == FLEXATT_BF16) &&
+         (p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256);
 }
 BwdLauncher pick_kv_ds(const flexatt_problem* p) {
-  if (p->head_dim == 64) return p->dtype == FLEXATT_BF16 ? bwd_kv_ds_bf16_d64 : bwd_kv_ds_f16_d64;
-  return p->dtype == FLEXATT_BF16 ? bwd_kv_ds_bf16_d128 : bwd_kv_ds_f16_d128;
+  const bool bf = p->dtype == FLEXATT_BF16;
+  if (p->head_dim == 64) return bf ? bwd_kv_ds_bf16_d64 : bwd_kv_ds_f16_d64;
+  if (p->head_dim == 256) return bf ? bwd_kv_ds_bf16_d256 : bwd_kv_ds_f16_d256;
+  return bf ? bwd_kv_ds_bf16_d128 : bwd_kv_ds_f16_d128;
 }
 BwdLauncher pick_dq_ds(const flexatt_problem* p) {
-  if (p->head_dim == 64) return p->dtype == FLEXATT_BF16 ? bwd_dq_ds_bf16_d64 : bwd_dq_ds_f16_d64;
-  return p->dtype == FLEXATT_BF16 ? bwd_dq_ds_bf16_d128 : bwd_dq_ds_f16_d128;
+  const bool bf = p->dtype == FLEXATT_BF16;
+  if (p->head_dim == 64) return bf ? bwd_dq_ds_bf16_d64 : bwd_dq_ds_f16_d64;
+  if (p->head_dim == 256) return bf ? bwd_dq_ds_bf16_d256 : bwd_dq_ds_f16_d256;
+  return bf ? bwd_dq_ds_bf16_d128 : bwd_dq_ds_f16_d128;
 }
 int64_t ds_units_per_head(const flexatt_problem* p) {
   const int nqt = (p->seqlen_q + kDsQT - 1) / kDsQT;

@@ -191,10 +191,12 @@ __device__ __forceinline__ int swz_tr_inv(int r, int p) {
 //    16 rows, and rows 4i, 4i+2 (and 4i+1, 4i+3) differ in bit 2 of g, so
 //    their 4-chunk groups fall in different halves of the bank row.
 // The swizzle is its own inverse.
+//  * 512-byte rows (CPR 32, a row spans two bank rows, group = chunk mod
+//    16): the CPR 16 map on the low four chunk bits.
 template <int CPR>
 __device__ __forceinline__ int swz_dual(int r, int c) {
-  static_assert(CPR == 16 || CPR == 8, "dual-use swizzle is defined for 256- and 128-byte rows");
-  if constexpr (CPR == 16) return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
+  static_assert(CPR == 32 || CPR == 16 || CPR == 8, "dual-use swizzle is defined for 512-, 256- and 128-byte rows");
+  if constexpr (CPR >= 16) return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
   else return c ^ ((((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 1) | ((r >> 2) & 1));
 }
 template <int CPR>

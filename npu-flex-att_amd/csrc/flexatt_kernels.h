@@ -83,14 +83,16 @@ hipError_t fwd_decode_f16_d64(const DecodeArgs&, hipStream_t);
 hipError_t fwd_decode_bf16_d128(const DecodeArgs&, hipStream_t);
 hipError_t fwd_decode_f16_d128(const DecodeArgs&, hipStream_t);
 
-// dK/dV as a KV-stationary tile stream (bwd_kv.hip), D = 128 and 64.
+// dK/dV as a KV-stationary tile stream (bwd_kv.hip), D = 64, 128 and 256.
 hipError_t bwd_kv_bf16_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_f16_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_bf16_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_f16_d64(const BwdArgs&, hipStream_t);
+hipError_t bwd_kv_bf16_d256(const BwdArgs&, hipStream_t);  // two launches: dV, then dK
+hipError_t bwd_kv_f16_d256(const BwdArgs&, hipStream_t);
 
 // dK/dV that also writes its dS to a.ds (bwd_kv.hip), and dQ = scale * dS K
-// from it (bwd_dq_ds.hip), D = 128 and 64.
+// from it (bwd_dq_ds.hip), D = 64, 128 and 256.
 hipError_t bwd_kv_ds_bf16_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_ds_f16_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_bf16_d128(const BwdArgs&, hipStream_t);
@@ -99,6 +101,10 @@ hipError_t bwd_kv_ds_bf16_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_ds_f16_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_bf16_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_f16_d64(const BwdArgs&, hipStream_t);
+hipError_t bwd_kv_ds_bf16_d256(const BwdArgs&, hipStream_t);
+hipError_t bwd_kv_ds_f16_d256(const BwdArgs&, hipStream_t);
+hipError_t bwd_dq_ds_bf16_d256(const BwdArgs&, hipStream_t);
+hipError_t bwd_dq_ds_f16_d256(const BwdArgs&, hipStream_t);
 
 // dQ as a query-stationary tile stream (bwd_q.hip), D = 128; with
 // a.delta_out set it also computes Delta (written there) from O and dO.

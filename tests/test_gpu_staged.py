@@ -1,6 +1,6 @@
 """GPU tests of the backward with dS staged through HBM (flexatt_bwd_ws: the
 dK/dV kernel writes its rounded dS, the dQ kernel streams dS K), the path
-npu_flash_attention_backward takes for fp16/bf16 with head_dim 128 or 64.
+npu_flash_attention_backward takes for fp16/bf16 with head_dim 64, 128 or 256.
 
 * the five outputs against the float64 oracle at the north-star bounds, over
   GQA ratios 1, 2, 3, 4, 7 and 8 (head groups that do not fill a workgroup),
@@ -42,6 +42,13 @@ CASES = {
     "d64_bf16_g1_full_sq_lt_skv": (torch.bfloat16, 2, 2, 2, 200, 333, dict(d=64)),
     "d64_fp16_g4_window": (torch.float16, 1, 8, 2, 1000, 1000, dict(sliding_window=300, d=64)),
     "d64_fp16_g2_one_key": (torch.float16, 1, 4, 2, 65, 1, dict(d=64)),
+    # head_dim 256 (dV and dK in two passes)
+    "d256_bf16_g2_causal_window_cap": (torch.bfloat16, 1, 4, 2, 600, 600,
+                                       dict(causal=True, sliding_window=300, soft_cap=50.0, scale=1 / 16, d=256)),
+    "d256_fp16_g3_all_sq_gt_skv": (torch.float16, 1, 6, 2, 333, 257,
+                                   dict(causal=True, alibi=True, soft_cap=20.0, scale=0.05, d=256)),
+    "d256_bf16_g1_full": (torch.bfloat16, 2, 2, 2, 200, 300, dict(d=256)),
+    "d256_fp16_g8_one_key": (torch.float16, 1, 8, 1, 40, 1, dict(d=256)),
 }
 
 
@@ -72,7 +79,7 @@ def test_staged_matches_oracle(gpu_device, case):
 
 
 @pytest.mark.parametrize("case", ["bf16_g3_causal", "fp16_g1_window_alibi_cap", "bf16_g7_causal_sq_gt_skv",
-                                  "d64_fp16_g7_all"])
+                                  "d64_fp16_g7_all", "d256_fp16_g3_all_sq_gt_skv"])
 def test_staged_ds_values(gpu_device, case):
     """Decode the workspace: unit (b, h, t, kb) fragment f, lane l, element e
     holds dS/scale of query row 32 t + l % 32 and KV row
@@ -123,7 +130,8 @@ def test_staged_ds_values(gpu_device, case):
     assert e <= tol, f"staged dS err {e:.3e} > {tol}"
 
 
-@pytest.mark.parametrize("case", ["bf16_g8_causal_window", "fp16_g7_full_sq_lt_skv", "bf16_g4_all", "d64_fp16_g4_window"])
+@pytest.mark.parametrize("case", ["bf16_g8_causal_window", "fp16_g7_full_sq_lt_skv", "bf16_g4_all", "d64_fp16_g4_window",
+                                  "d256_bf16_g2_causal_window_cap"])
 def test_staged_against_recompute_path(gpu_device, case):
     dtype, cpu, (q, k, v, do), kw = _inputs(case)
     o, lse = nfa.npu_flash_attention_forward(q, k, v, return_lse=True, **kw)
@@ -141,7 +149,8 @@ def test_staged_against_recompute_path(gpu_device, case):
         check(name, x, r.double(), dtype)
 
 
-@pytest.mark.parametrize("case", ["bf16_g3_causal", "fp16_g1_window_alibi_cap", "d64_bf16_g3_causal"])
+@pytest.mark.parametrize("case", ["bf16_g3_causal", "fp16_g1_window_alibi_cap", "d64_bf16_g3_causal",
+                                  "d256_bf16_g1_full"])
 def test_staged_kernels_and_repeats_bitwise(gpu_device, case):
     dtype, cpu, (q, k, v, do), kw = _inputs(case)
     lib = L.load()
@@ -184,7 +193,7 @@ def test_staged_kernels_and_repeats_bitwise(gpu_device, case):
     assert torch.equal(c[1], c[4]) and torch.equal(c[2], c[5]), "staging changed dK/dV"
 
 
-@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("d", [128, 64, 256])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 def test_staged_fully_masked_rows(gpu_device, dtype, d):
     """Non-causal window W = 30 over Skv = 100 keys: query rows >= 131 see
