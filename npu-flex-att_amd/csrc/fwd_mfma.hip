@@ -39,7 +39,10 @@ namespace flexatt {
 template <int D>
 struct FwdCfg {
   static constexpr int NW = D <= 128 ? 8 : 4;   // waves per workgroup
-  static constexpr int WPE = D <= 128 ? 2 : 1;  // waves per SIMD the register budget targets
+  // waves per SIMD the register budget targets: at D = 64 two workgroups
+  // share a CU (64 KB of LDS each), whose VALU-heavy phases then overlap
+  // (D = 32 would spill at that budget)
+  static constexpr int WPE = D == 64 ? 4 : (D <= 128 ? 2 : 1);
 #ifdef FLEXATT_FWD_BN
   static constexpr int BN = FLEXATT_FWD_BN;  // tuning override
 #else
