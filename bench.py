@@ -68,6 +68,9 @@ def parse():
     ap.add_argument("--no-gemm-peak", action="store_true", help="skip the plain bf16 GEMM reference rate")
     ap.add_argument("--recompute-dq", action="store_true",
                     help="backward without dS staging: the dQ kernel recomputes S and dP (flexatt_bwd)")
+    ap.add_argument("--block-sparsity", type=float, default=0.0,
+                    help="also pass a block-sparse map (128 x 128 blocks, shared by all heads) with this fraction "
+                         "of the off-diagonal blocks removed; FLOPs count the remaining pairs")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one 256 MiB device copy (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -136,6 +139,14 @@ def main():
     if alibi:
         slopes = torch.tensor([2.0 ** (-8.0 * (h + 1) / Hq) for h in range(Hq)], dtype=torch.float32, device=dev)
     kw = dict(causal=causal, sliding_window=window, soft_cap=cap, scale=scale, alibi_slope=slopes)
+    masks = None
+    if args.block_sparsity > 0:
+        nqb, nkb = -(-Sq // 128), -(-Skv // 128)
+        gb = torch.Generator().manual_seed(7)
+        keep = torch.rand(nqb, nkb, generator=gb) >= args.block_sparsity
+        keep |= torch.eye(nqb, nkb, dtype=torch.bool)  # every row keeps its diagonal block
+        kw["block_mask"] = keep.to(torch.uint8).view(1, 1, nqb, nkb).to(dev)
+        masks = nfa._masks(causal, None, None, kw["block_mask"], B, Hq, Sq, Skv, dev)
 
     if args.copy_probe:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -146,6 +157,16 @@ def main():
         del src, dst
 
     npairs = pairs(Sq, Skv, causal, window)
+    if masks is not None:  # pairs of the kept blocks only
+        i = torch.arange(Sq).view(-1, 1)
+        j = torch.arange(Skv).view(1, -1)
+        ok = torch.ones(Sq, Skv, dtype=torch.bool)
+        if causal:
+            ok &= j <= i
+        if window > 0:
+            ok &= i - j <= window
+        ok &= keep.repeat_interleave(128, 0).repeat_interleave(128, 1)[:Sq, :Skv]
+        npairs = int(ok.sum())
     fwd_flop = 4.0 * D * npairs * B * Hq
     bwd_flop = 2.5 * fwd_flop
 
@@ -173,7 +194,7 @@ def main():
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
-    p = nfa._problem(q, k, scale if scale is not None else 1.0 / math.sqrt(D), causal, window, cap, slopes)
+    p = nfa._problem(q, k, scale if scale is not None else 1.0 / math.sqrt(D), causal, window, cap, slopes, masks)
     st = torch.cuda.current_stream(dev)
     sh = st.cuda_stream
     T = L.tensor
@@ -238,7 +259,8 @@ def main():
         "data": "synthetic N(0,1), seed 42, resident in HBM",
         "config": {
             "workload": f"{args.config}: {dts} B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} Skv={Skv} D={D} causal={causal} "
-                        f"window={window} soft_cap={cap} alibi={alibi} scale={scale}; step = fwd + bwd",
+                        f"window={window} soft_cap={cap} alibi={alibi} scale={scale}"
+                        + (f" block_sparsity={args.block_sparsity}" if masks is not None else "") + "; step = fwd + bwd",
             "batch": B, "heads_q": Hq, "heads_kv": Hkv, "seqlen_q": Sq, "seqlen_kv": Skv, "head_dim": D,
             "parallelism": "single GPU", "layout": args.layout,
         },
@@ -257,7 +279,7 @@ def main():
             "peak": PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_TFLOPS, 4),
-            "traffic": recorded_traffic(args.config, dom),
+            "traffic": recorded_traffic(args.config, dom) if masks is None else None,
         },
         "cpu_baseline": cpu,
     }

@@ -140,6 +140,24 @@ void bwd_dq_ds_kernel(BwdArgs a) {
     }
   }
 
+  // Block-sparse maps: the block-map row of each of this wave's slots over
+  // the workgroup's KV blocks, in (dynamic) LDS, so that the loop issues no
+  // memory operation besides its own loads; a slot skips the MFMAs of
+  // sub-blocks in removed blocks and loads a cached address instead of their
+  // (zero) dS.
+  extern __shared__ unsigned char sblk[];
+  constexpr int SPB = kBlk / C::SB;  // sub-blocks per block
+  const int kb0 = g_lo / SPB, nkbw = nsub > 0 ? (g_hi - 1) / SPB - kb0 + 1 : 0;
+  unsigned char* myblk = sblk + wave * C::NSL * kBlkRowMax;
+  if (p.blk) {
+#pragma unroll
+    for (int c = 0; c < C::NSL; ++c) {
+      const unsigned char* row = block_row(p, b, hq_c[c], min(t_c[c] * kDsQT, p.Sq - 1));
+      for (int i = lane; i < nkbw; i += 64) myblk[c * kBlkRowMax + i] = row[kb0 + i];
+    }
+  }
+  auto live = [&](int c, int s) { return !p.blk || myblk[c * kBlkRowMax + s / SPB - kb0] != 0; };
+
   // K copies: chunk q = (wave EK + e) 64 + lane of the sub-block, row q / CPR,
   // at its swizzled chunk (the dual-use swizzle of the backward tiles).
   int krow[C::EK], kchk[C::EK];
@@ -164,7 +182,7 @@ void bwd_dq_ds_kernel(BwdArgs a) {
     const int s = g_lo + i;
 #pragma unroll
     for (int c = 0; c < C::NSL; ++c) {
-      const bool in = s >= s_lo[c] && s < s_hi[c];
+      const bool in = s >= s_lo[c] && s < s_hi[c] && live(c, s);
       const char* src = in ? dsrc[c] + (int64_t)(s / SPU - s_lo[c] / SPU) * kDsUnitB + (s % SPU) * C::SUBB
                            : dsrc[c];
 #pragma unroll
@@ -219,7 +237,7 @@ void bwd_dq_ds_kernel(BwdArgs a) {
     const int s = g_lo + i;
     bool on[C::NSL];
 #pragma unroll
-    for (int c = 0; c < C::NSL; ++c) on[c] = s >= s_lo[c] && s < s_hi[c];
+    for (int c = 0; c < C::NSL; ++c) on[c] = s >= s_lo[c] && s < s_hi[c] && live(c, s);
     const char* sK = smem + (i & (C::KSTAGES - 1)) * C::KTILEB;
     // 16 (k step, d-block) operand reads, each feeding one MFMA per slot
     i16x4 alo[3], ahi[3];
@@ -293,7 +311,8 @@ hipError_t launch_dq_ds(const BwdArgs& a, hipStream_t st) {
   const int nqb = (nqt + nq - 1) / nq;
   x.ntiles = (nqb << 8) | nh;
   const dim3 grid(nqb * (a.p.G / nh) * a.p.B * a.p.Hkv), block(C::NW * 64);
-  hipLaunchKernelGGL((bwd_dq_ds_kernel<T, D>), grid, block, 0, st, x);
+  const size_t dyn = a.p.blk ? (size_t)C::NW * C::NSL * kBlkRowMax : 0;  // block-map rows of the slots
+  hipLaunchKernelGGL((bwd_dq_ds_kernel<T, D>), grid, block, dyn, st, x);
   return hipGetLastError();
 }
 

@@ -199,20 +199,29 @@ void bwd_kv_kernel(BwdArgs a) {
     }
     int cg = 0, cqt = qt_top;  // tile being formed (head, query tile)
     int sc = 0;               // its stage
+    // Block-sparse maps: the byte of tile u's 128 x 128 block, loaded one
+    // step ahead (the S-wave has no other memory operation in flight, so the
+    // wait at its use is for this load alone).  A removed tile skips the
+    // S-wave's MFMAs and VALU work: its P and dS are written as zeros.
+    auto blk_byte = [&](int g, int qt) -> int {
+      return block_row(p, b, hk * p.G + g, min(qt * C::BM, p.Sq - 1))[min(kw0, p.Skv - 1) / kBlk];
+    };
+    int blk_next = 1;
+    if (p.blk && ntile > 0) blk_next = blk_byte(0, qt_top);
 
     __syncthreads();  // prologue: tile 0 landed
     for (int u = 0; u <= ntile; ++u) {
       const bool act = u < ntile;
       f32x16 S, DP;        // Q K^T and Delta - dO V^T (the latter accumulated from Delta)
       f32x4 L4[4];         // LSE (to log2 units) of this lane's query rows
-      // block-sparse mask: whether tile u's 128 x 128 block is computed (read
-      // here, used in V(u); the S-wave has no other memory operation in flight)
       bool live = true;
-      if (p.blk && act)
-        live = __builtin_amdgcn_readfirstlane(block_on(p, b, hk * p.G + cg, min(cqt * C::BM, p.Sq - 1),
-                                                       min(kw0, p.Skv - 1)));
+      if (p.blk && act) {
+        live = __builtin_amdgcn_readfirstlane(blk_next) != 0;
+        const int ng = cg + 1 == p.G ? 0 : cg + 1, nqt = cg + 1 == p.G ? cqt - 1 : cqt;
+        if (u + 1 < ntile) blk_next = blk_byte(ng, nqt);
+      }
       // ---- M(u): S = Q K^T, DP = Delta - dO V^T of tile u; LSE reads ------
-      if (act) {
+      if (act && live) {
         // Row-read addresses of this stage (the Q / dO choice folds into the
         // instruction offset).
         int ra[C::KC];
@@ -296,7 +305,7 @@ void bwd_kv_kernel(BwdArgs a) {
             if constexpr (decltype(masked)::value) {
               const int q = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
               const bool ok = (q < p.Sq) & (my_kv < p.Skv) & (!p.causal | (my_kv <= q)) &
-                              ((p.window == 0) | (q - my_kv <= p.window)) & (q >= clo) & (q < chi) & live;
+                              ((p.window == 0) | (q - my_kv <= p.window)) & (q >= clo) & (q < chi);
               e = ok ? e : 0.f;
             }
             pe[r] = e;
@@ -320,11 +329,21 @@ void bwd_kv_kernel(BwdArgs a) {
             *(V8*)xslot(u, SLOT_DS + 1) = pack8<T>(de, 8);
           }
         };
-        if ((m0 + C::BM > p.Sq) || kv_tail || (p.causal && m0 < kw0 + 31) ||
-            (p.window > 0 && m0 + C::BM - 1 - kw0 > p.window) || m0 < pc_lo || m0 + C::BM > pc_hi || !live)
+        if (!live) {
+          if constexpr (DOV) {
+            *(V8*)xslot(u, SLOT_P) = V8{};
+            *(V8*)xslot(u, SLOT_P + 1) = V8{};
+          }
+          if constexpr (DOK) {
+            *(V8*)xslot(u, SLOT_DS) = V8{};
+            *(V8*)xslot(u, SLOT_DS + 1) = V8{};
+          }
+        } else if ((m0 + C::BM > p.Sq) || kv_tail || (p.causal && m0 < kw0 + 31) ||
+                   (p.window > 0 && m0 + C::BM - 1 - kw0 > p.window) || m0 < pc_lo || m0 + C::BM > pc_hi) {
           form(std::true_type{});
-        else
+        } else {
           form(std::false_type{});
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();  // Y(u)

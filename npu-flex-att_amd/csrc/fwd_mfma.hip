@@ -27,6 +27,10 @@
 //  * Only tiles that straddle a mask edge or the KV tail evaluate the mask per
 //    element; fully masked blocks of such tiles run the same instructions
 //    with P = 0 (one straight path keeps the accumulators in place).
+//  * Block-sparse maps: a wave skips the softmax of tiles in removed
+//    128 x 128 blocks of its rows and feeds P = 0 to their PV MFMAs (a
+//    branch around the MFMA phase costs the ping-pong loop its register
+//    budget); the 4-wave form (D = 256) skips such tiles entirely.
 #include "flexatt_device.h"
 #include "flexatt_kernels.h"
 
@@ -370,6 +374,11 @@ void fwd_mfma_kernel(FwdArgs a) {
     tm_hi = __builtin_amdgcn_readfirstlane(tm_hi);
     tm_lo = __builtin_amdgcn_readfirstlane(tm_lo);
     auto softmax = [&](int n0) {
+      if (!block_live(n0)) {  // a removed block: P = 0 for the PV MFMAs, if they run
+#pragma unroll
+        for (int i = 0; i < 2 * C::NB; ++i) P[i] = V8{};
+        return;
+      }
       if constexpr (!RAW) {
         // i - j = fb - (32 bb + 8 (r / 4) + r % 4), exact in fp32
         const float fb = (float)(my_m - n0 - 4 * h);
@@ -534,7 +543,7 @@ void fwd_mfma_kernel(FwdArgs a) {
       // window edge or the KV tail for some row of this wave.
       const bool need_mask = (n0 + C::BN > p.Skv) || (p.causal && n0 + C::BN - 1 > mw) ||
                              (p.window > 0 && mw + 31 - n0 > p.window) || p.doc || !block_live(n0);
-      tile_body(sK, sV, n0, need_mask);
+      if (block_live(n0)) tile_body(sK, sV, n0, need_mask);  // removed blocks are skipped
       st = st == 2 ? 0 : st + 1;
     }
   }
