@@ -132,6 +132,13 @@ void fwd_mfma_kernel(FwdArgs a) {
   }
   const int t_lo = kv_lo / C::BN;
   const int t_hi = (kv_hi + C::BN - 1) / C::BN;
+  // This lane's row attends to the keys [row_lo, row_lo + row_w): causal,
+  // window, KV tail and document bounds as one interval, so that a masked
+  // tile tests each element with one unsigned compare against its offset.
+  int row_lo = max(dlo, 0), row_hi = min(dhi, p.Skv);
+  if (p.causal) row_hi = min(row_hi, my_m + 1);
+  if (p.window > 0) row_lo = max(row_lo, my_m - p.window);
+  const unsigned row_w = (unsigned)max(row_hi - row_lo, 0);
 
   // Block-sparse mask: this wave's row of the block map over the
   // workgroup's KV range, kept in (dynamic) LDS so that the tile loop issues
@@ -227,15 +234,13 @@ void fwd_mfma_kernel(FwdArgs a) {
                                                  fb - (float)(32 * bb + 8 * (r >> 2) + (r & 3)), tv);
         }
     }
-    if (need_mask) {
-      const bool live = block_live(n0);
+    if (need_mask) {  // (removed blocks never get here)
+      const int a0 = row_lo - n0 - 4 * h;  // element offset of the interval's start
 #pragma unroll
       for (int bb = 0; bb < C::NB; ++bb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (!live || !allowed(p, my_m, j) || j < dlo || j >= dhi) s[bb][r] = kNegInf;
-        }
+        for (int r = 0; r < 16; ++r)
+          if ((unsigned)(32 * bb + 8 * (r >> 2) + (r & 3) - a0) >= row_w) s[bb][r] = kNegInf;
     }
 
     // tile row max (pairwise tree), exchanged between the wave halves
@@ -392,15 +397,14 @@ void fwd_mfma_kernel(FwdArgs a) {
           }
       }
       const int tn = n0 / C::BN;
-      const bool live = block_live(n0);
-      if (tn < tm_lo || tn >= tm_hi || !live) {
+      if (tn < tm_lo || tn >= tm_hi) {
+        // element (bb, r) is key n0 + 32 bb + 8 (r / 4) + 4 h + r % 4
+        const int a0 = row_lo - n0 - 4 * h;
 #pragma unroll
         for (int bb = 0; bb < C::NB; ++bb) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int j = n0 + 32 * bb + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (!live || !allowed(p, my_m, j) || j < dlo || j >= dhi) s[bb][r] = kNegInf;
-          }
+          for (int r = 0; r < 16; ++r)
+            if ((unsigned)(32 * bb + 8 * (r >> 2) + (r & 3) - a0) >= row_w) s[bb][r] = kNegInf;
           pin(s[bb]);  // finished inside the branch (no selects after it)
         }
       }
