@@ -197,6 +197,15 @@ void bwd_kv_kernel(BwdArgs a) {
       pc_lo = l1;
       pc_hi = h0;
     }
+    // The query rows this lane's KV row may meet, as one interval
+    // [q_lo, q_lo + q_w): causal, window, query tail, KV tail and column
+    // bounds, so that a masked tile tests each element with one unsigned
+    // compare against its offset.
+    int q_lo = max(clo, 0), q_hi = min(chi, p.Sq);
+    if (p.causal) q_lo = max(q_lo, my_kv);
+    if (p.window > 0) q_hi = min(q_hi, my_kv + p.window + 1);
+    if (my_kv >= p.Skv) q_hi = q_lo;
+    const unsigned q_w = (unsigned)max(q_hi - q_lo, 0);
     int cg = 0, cqt = qt_top;  // tile being formed (head, query tile)
     int sc = 0;               // its stage
     // Block-sparse maps: the byte of tile u's 128 x 128 block, loaded one
@@ -303,10 +312,8 @@ void bwd_kv_kernel(BwdArgs a) {
           for (int r = 0; r < 16; ++r) {
             float e = fast_exp2(y[r]);
             if constexpr (decltype(masked)::value) {
-              const int q = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
-              const bool ok = (q < p.Sq) & (my_kv < p.Skv) & (!p.causal | (my_kv <= q)) &
-                              ((p.window == 0) | (q - my_kv <= p.window)) & (q >= clo) & (q < chi);
-              e = ok ? e : 0.f;
+              const int a0 = q_lo - m0 - 4 * h;  // element offset of the interval's start
+              e = (unsigned)(8 * (r >> 2) + (r & 3) - a0) < q_w ? e : 0.f;
             }
             pe[r] = e;
           }
