@@ -555,19 +555,34 @@ void fwd_mfma_kernel(FwdArgs a) {
   const float l_tot = l_run + swap_halves(l_run);
   const bool empty = !(l_tot > 0.f);
   const float inv = empty ? 0.f : 1.0f / l_tot;
-  if (my_m < p.Sq) {
-    T* op = (T*)a.o.data + b * a.o.sb + hq * a.o.sh + (int64_t)my_m * a.o.ss + 4 * h;
+  // O leaves through LDS: each lane holds 4 columns of one row, which would
+  // make every store instruction touch 32 rows; staged as the wave's 32 x D
+  // row-major tile (16-byte chunk c of row r at c ^ (r % CPR)), it is stored
+  // 16 contiguous bytes per lane, 64 / CPR whole rows per instruction.
+  if constexpr (!C::PP) __syncthreads();  // the last tile's LDS reads are done
+  char* so = smem + wave * 32 * C::ROWB;
 #pragma unroll
-    for (int db = 0; db < C::DB; ++db) {
+  for (int db = 0; db < C::DB; ++db) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        st_global8(op + 32 * db + 8 * i,
-                   pack4<T>(acc[db][4 * i] * inv, acc[db][4 * i + 1] * inv, acc[db][4 * i + 2] * inv,
-                            acc[db][4 * i + 3] * inv));
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int c = 4 * db + i;  // columns 32 db + 8 i .. + 7; this lane's half at byte 8 h
+      *(i32x2*)(so + l32 * C::ROWB + (c ^ (l32 % C::CPR)) * 16 + 8 * h) =
+          pack4<T>(acc[db][4 * i] * inv, acc[db][4 * i + 1] * inv, acc[db][4 * i + 2] * inv, acc[db][4 * i + 3] * inv);
     }
-    if (h == 0) a.lse[(int64_t)(b * p.Hq + hq) * p.Sq + my_m] = empty ? kNegInf : (m_run + log2f(l_tot)) * kLn2;
   }
+  {
+    constexpr int RPI = 64 / C::CPR;  // rows per store instruction
+    const int cc = lane % C::CPR;
+    T* ob = (T*)a.o.data + b * a.o.sb + hq * a.o.sh + cc * 8;
+#pragma unroll
+    for (int k = 0; k < 32 / RPI; ++k) {
+      const int rr = k * RPI + lane / C::CPR;
+      const i32x4 x = lds_read16(so + rr * C::ROWB + (cc ^ (rr % C::CPR)) * 16);
+      if (mw + rr < p.Sq) *(i32x4*)(ob + (int64_t)(mw + rr) * a.o.ss) = x;
+    }
+  }
+  if (my_m < p.Sq && h == 0)
+    a.lse[(int64_t)(b * p.Hq + hq) * p.Sq + my_m] = empty ? kNegInf : (m_run + log2f(l_tot)) * kLn2;
 }
 
 // Heads per workgroup: the largest power of two that divides G, capped at NW.
