@@ -81,10 +81,14 @@ void bwd_dq_ds_kernel(BwdArgs a) {
   const int nh = a.ntiles & 0xff;  // heads per workgroup: 4, 2 or 1 (divides G)
   const int nqb = a.ntiles >> 8;   // query blocks per head group
   const int nq = C::SLOTS / nh;    // query tiles per block
-  const int w = xcd_remap(blockIdx.x, gridDim.x);
-  const int qb = nqb - 1 - (w % nqb);
-  int rest = w / nqb;
   const int ngs = p.G / nh;
+  int kq, rest;  // kq = 0: the last query block, the longest causal band
+  if (!xcd_lpt_item(blockIdx.x, nqb, ngs * p.B * p.Hkv, kq, rest)) {
+    const int w = xcd_remap(blockIdx.x, gridDim.x);
+    kq = w % nqb;
+    rest = w / nqb;
+  }
+  const int qb = nqb - 1 - kq;
   const int hg = rest % ngs;
   rest /= ngs;
   const int hk = rest % p.Hkv, b = rest / p.Hkv;

@@ -124,8 +124,12 @@ void bwd_kv_kernel(BwdArgs a) {
   // Work item: (b, hkv, KV block), blocks of one (b, hkv) consecutive so that
   // they share an XCD (and its L2) and heavy / light causal blocks interleave.
   const int nkb = a.ntiles;
-  const int w = xcd_remap(blockIdx.x, gridDim.x);
-  const int kb = w % nkb, bh = w / nkb;
+  int kb, bh;  // block 0 has the longest causal band
+  if (!xcd_lpt_item(blockIdx.x, nkb, p.B * p.Hkv, kb, bh)) {
+    const int w = xcd_remap(blockIdx.x, gridDim.x);
+    kb = w % nkb;
+    bh = w / nkb;
+  }
   const int hk = bh % p.Hkv, b = bh / p.Hkv;
   const int n0 = kb * C::BKV;
   const int kw0 = n0 + 32 * pr;  // first KV row of this pair

@@ -89,10 +89,14 @@ void fwd_mfma_kernel(FwdArgs a) {
   // Work item: (b, hkv, head group, q-tile); the longest causal tiles first.
   const int gp = a.gpack;
   const int bmh = 32 * (C::NW / gp);  // query rows per head
-  const int w = xcd_remap(blockIdx.x, gridDim.x);
-  const int qt = a.nqt - 1 - (w % a.nqt);
-  int rest = w / a.nqt;
   const int ngs = p.G / gp;
+  int kq, rest;  // kq = 0: the last query tile, the longest causal band
+  if (!xcd_lpt_item(blockIdx.x, a.nqt, ngs * p.B * p.Hkv, kq, rest)) {
+    const int w = xcd_remap(blockIdx.x, gridDim.x);
+    kq = w % a.nqt;
+    rest = w / a.nqt;
+  }
+  const int qt = a.nqt - 1 - kq;
   const int gs = rest % ngs;
   rest /= ngs;
   const int hk = rest % p.Hkv, b = rest / p.Hkv;
