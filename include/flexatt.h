@@ -176,23 +176,30 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
                 const float* lse, float* delta, const flexatt_tensor* dq, const flexatt_tensor* dk,
                 const flexatt_tensor* dv, void* stream);
 
+/* Bytes of work-queue counters at the end of the staged-dS workspace. */
+#define FLEXATT_BWD_QUEUE_BYTES 256
+
 /* Backward with dS staged through HBM (fp16/bf16, head_dim 64, 128 or 256).  The dK/dV kernel already forms dS for every attended
  * pair; it writes those values (rounded to the input dtype, as its own dK
  * MFMAs consume them) to a caller-owned workspace, and the dQ kernel forms
  * dQ = scale * dS K from them instead of recomputing S and dP.  The
  * workspace holds 2 bytes per attended (query row, KV row) pair of each
  * query head, in 32 x 128 units over the causal / window band (interval
- * and block masks keep that band; their masked pairs hold zeros):
- * flexatt_bwd_workspace(p) bytes (0: the problem is outside this range),
- * 16-byte aligned, not zeroed, reusable once the call's work on `stream` is
- * done.  Same results as flexatt_bwd up to fp32 summation order; bitwise
- * deterministic.
+ * and block masks keep that band; their masked pairs hold zeros),
+ * followed by FLEXATT_BWD_QUEUE_BYTES of work-queue counters:
+ * flexatt_bwd_workspace(p) bytes in all (0: the problem is outside this
+ * range), 16-byte aligned, not zeroed, reusable once the call's work on
+ * `stream` is done.  Same results as flexatt_bwd up to fp32 summation
+ * order; bitwise deterministic.
  *
  * flexatt_bwd_ws: the whole backward (replaces the Delta op, both kernel
  * launches and the group sum of npu_flash_attention_backward,
  * npu_flash_attention.py:681-737): the Delta pass into `delta`, dK/dV
- * writing dS, then dQ.  Outside the range it runs flexatt_bwd and the
- * workspace may be NULL. */
+ * writing dS, then dQ.  Past the first workgroup per CU, the dK/dV and dQ
+ * workgroups take the longest remaining work items from the queue counters
+ * (which the Delta pass clears), so that faster XCDs take more work; with a
+ * workspace of only the dS band's size the static order is kept.  Outside
+ * the range it runs flexatt_bwd and the workspace may be NULL. */
 size_t flexatt_bwd_workspace(const flexatt_problem* p);
 int flexatt_bwd_ws(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
                    const flexatt_tensor* v, const flexatt_tensor* o, const flexatt_tensor* dout,
@@ -204,7 +211,8 @@ int flexatt_bwd_ws(const flexatt_problem* p, const flexatt_tensor* q, const flex
  * launch and the group sum (npu_flash_attention.py:714-737) and also fills
  * the workspace; flexatt_bwd_dq_ds replaces the flash_attn_bwd_dq_kernel
  * launch (:695-712) and reads the workspace a flexatt_bwd_dkdv_ds call on
- * the same problem wrote before it on the stream. */
+ * the same problem wrote before it on the stream.  Both keep the static work
+ * order (the queue counters are not used). */
 int flexatt_bwd_dkdv_ds(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
                         const flexatt_tensor* v, const flexatt_tensor* dout, const float* lse,
                         const float* delta, const flexatt_tensor* dk, const flexatt_tensor* dv,

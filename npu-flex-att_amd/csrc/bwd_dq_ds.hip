@@ -82,9 +82,11 @@ void bwd_dq_ds_kernel(BwdArgs a) {
   const int nqb = a.ntiles >> 8;   // query blocks per head group
   const int nq = C::SLOTS / nh;    // query tiles per block
   const int ngs = p.G / nh;
+  const int slot = queue_slot(a.queue, a.nstatic);
+  if (slot >= (int)gridDim.x) return;  // (a counter that was not cleared)
   int kq, rest;  // kq = 0: the last query block, the longest causal band
-  if (!xcd_lpt_item(blockIdx.x, nqb, ngs * p.B * p.Hkv, kq, rest)) {
-    const int w = xcd_remap(blockIdx.x, gridDim.x);
+  if (!xcd_lpt_item(slot, nqb, ngs * p.B * p.Hkv, kq, rest)) {
+    const int w = xcd_remap(slot, gridDim.x);
     kq = w % nqb;
     rest = w / nqb;
   }

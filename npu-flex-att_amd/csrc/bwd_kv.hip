@@ -124,9 +124,11 @@ void bwd_kv_kernel(BwdArgs a) {
   // Work item: (b, hkv, KV block), blocks of one (b, hkv) consecutive so that
   // they share an XCD (and its L2) and heavy / light causal blocks interleave.
   const int nkb = a.ntiles;
+  const int slot = queue_slot(a.queue, a.nstatic);
+  if (slot >= (int)gridDim.x) return;  // (a counter that was not cleared)
   int kb, bh;  // block 0 has the longest causal band
-  if (!xcd_lpt_item(blockIdx.x, nkb, p.B * p.Hkv, kb, bh)) {
-    const int w = xcd_remap(blockIdx.x, gridDim.x);
+  if (!xcd_lpt_item(slot, nkb, p.B * p.Hkv, kb, bh)) {
+    const int w = xcd_remap(slot, gridDim.x);
     kb = w % nkb;
     bh = w / nkb;
   }
@@ -637,6 +639,7 @@ hipError_t launch_kv(const BwdArgs& a, hipStream_t st) {
   auto go = [&](auto pass_c) {
     constexpr int PS = decltype(pass_c)::value;
     constexpr bool DSP = DS && PS != 1;
+    x.queue = a.queue ? a.queue + (PS == 2 ? 1 : 0) : nullptr;  // one counter per launch
     if (sc && al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, true, DSP, PS>), grid, block, 0, st, x);
     else if (sc) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, false, DSP, PS>), grid, block, 0, st, x);
     else if (al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, true, DSP, PS>), grid, block, 0, st, x);

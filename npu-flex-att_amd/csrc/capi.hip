@@ -276,6 +276,8 @@ int bwd_common(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_
   a.delta_out = nullptr;
   a.ds = nullptr;
   a.ds_head = 0;
+  a.queue = nullptr;
+  a.nstatic = 0;
   return FLEXATT_OK;
 }
 
@@ -308,6 +310,18 @@ size_t ds_bytes(const flexatt_problem* p) {
   if (!ds_applies(p)) return 0;
   return (size_t)((int64_t)p->batch * p->heads_q * ds_units_per_head(p) * kDsUnitB);
 }
+// CUs of the current device (cached per device), 0 if unknown.
+int cu_count() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 int ds_workspace(const flexatt_problem* p, void* ws, size_t bytes, BwdArgs& a) {
   if (!ds_applies(p)) return FLEXATT_ERANGE;
   if (!ws) return FLEXATT_EINVAL;
@@ -397,8 +411,9 @@ int flexatt_fwd_decode_noalloc(const flexatt_problem* p, const flexatt_tensor* q
   return decode_run(p, d, q, k, v, o, lse, ws, (hipStream_t)stream);
 }
 
-int flexatt_bwd_delta(const flexatt_problem* p, const flexatt_tensor* o, const flexatt_tensor* dout,
-                      float* delta, void* stream) {
+namespace {
+int run_delta(const flexatt_problem* p, const flexatt_tensor* o, const flexatt_tensor* dout, float* delta,
+              int* zero, void* stream) {
   FLEXATT_TRY(check_problem(p));
   FLEXATT_TRY(check_tensor(o, p->dtype));
   FLEXATT_TRY(check_tensor(dout, p->dtype));
@@ -411,7 +426,14 @@ int flexatt_bwd_delta(const flexatt_problem* p, const flexatt_tensor* o, const f
   a.H = p->heads_q;
   a.S = p->seqlen_q;
   a.D = p->head_dim;
+  a.zero = zero;
   return (int)bwd_delta(p->dtype, a, (hipStream_t)stream);
+}
+}  // namespace
+
+int flexatt_bwd_delta(const flexatt_problem* p, const flexatt_tensor* o, const flexatt_tensor* dout,
+                      float* delta, void* stream) {
+  return run_delta(p, o, dout, delta, nullptr, stream);
 }
 
 int flexatt_bwd_dq(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
@@ -473,13 +495,14 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
 
 size_t flexatt_bwd_workspace(const flexatt_problem* p) {
   if (check_problem(p) != FLEXATT_OK) return 0;
-  return ds_bytes(p);
+  const size_t n = ds_bytes(p);
+  return n ? n + FLEXATT_BWD_QUEUE_BYTES : 0;
 }
 
-int flexatt_bwd_dkdv_ds(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
-                        const flexatt_tensor* v, const flexatt_tensor* dout, const float* lse, const float* delta,
-                        const flexatt_tensor* dk, const flexatt_tensor* dv, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+namespace {
+int run_dkdv_ds(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k, const flexatt_tensor* v,
+                const flexatt_tensor* dout, const float* lse, const float* delta, const flexatt_tensor* dk,
+                const flexatt_tensor* dv, void* workspace, size_t workspace_bytes, int* queue, void* stream) {
   BwdArgs a;
   FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
   FLEXATT_TRY(check_out_tensor(dk, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
@@ -487,11 +510,13 @@ int flexatt_bwd_dkdv_ds(const flexatt_problem* p, const flexatt_tensor* q, const
   FLEXATT_TRY(ds_workspace(p, workspace, workspace_bytes, a));
   a.dk = mview(dk);
   a.dv = mview(dv);
+  a.queue = queue;
+  a.nstatic = cu_count() & ~7;
   return (int)pick_kv_ds(p)(a, (hipStream_t)stream);
 }
 
-int flexatt_bwd_dq_ds(const flexatt_problem* p, const flexatt_tensor* k, const void* workspace,
-                      size_t workspace_bytes, const flexatt_tensor* dq, void* stream) {
+int run_dq_ds(const flexatt_problem* p, const flexatt_tensor* k, const void* workspace, size_t workspace_bytes,
+              const flexatt_tensor* dq, int* queue, void* stream) {
   FLEXATT_TRY(check_problem(p));
   FLEXATT_TRY(check_tensor(k, p->dtype));
   FLEXATT_TRY(check_out_tensor(dq, p->dtype, p->batch, p->heads_q, p->seqlen_q, p->head_dim));
@@ -501,8 +526,23 @@ int flexatt_bwd_dq_ds(const flexatt_problem* p, const flexatt_tensor* k, const v
   a.p = make_shape(p);
   a.ntiles = 0;
   a.delta_out = nullptr;
+  a.queue = queue;
+  a.nstatic = cu_count() & ~7;
   FLEXATT_TRY(ds_workspace(p, (void*)workspace, workspace_bytes, a));
   return (int)pick_dq_ds(p)(a, (hipStream_t)stream);
+}
+}  // namespace
+
+int flexatt_bwd_dkdv_ds(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                        const flexatt_tensor* v, const flexatt_tensor* dout, const float* lse, const float* delta,
+                        const flexatt_tensor* dk, const flexatt_tensor* dv, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  return run_dkdv_ds(p, q, k, v, dout, lse, delta, dk, dv, workspace, workspace_bytes, nullptr, stream);
+}
+
+int flexatt_bwd_dq_ds(const flexatt_problem* p, const flexatt_tensor* k, const void* workspace,
+                      size_t workspace_bytes, const flexatt_tensor* dq, void* stream) {
+  return run_dq_ds(p, k, workspace, workspace_bytes, dq, nullptr, stream);
 }
 
 int flexatt_bwd_ws(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
@@ -518,9 +558,13 @@ int flexatt_bwd_ws(const flexatt_problem* p, const flexatt_tensor* q, const flex
   FLEXATT_TRY(check_out_tensor(dk, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
   FLEXATT_TRY(check_out_tensor(dv, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
   FLEXATT_TRY(ds_workspace(p, workspace, workspace_bytes, a));
-  FLEXATT_TRY(flexatt_bwd_delta(p, o, dout, delta, stream));
-  FLEXATT_TRY(flexatt_bwd_dkdv_ds(p, q, k, v, dout, lse, delta, dk, dv, workspace, workspace_bytes, stream));
-  return flexatt_bwd_dq_ds(p, k, workspace, workspace_bytes, dq, stream);
+  // queue counters after the dS band: [0], [1] the dK/dV launches, [2] dQ
+  int* queue = nullptr;
+  if (workspace_bytes >= ds_bytes(p) + FLEXATT_BWD_QUEUE_BYTES && (cu_count() & ~7) > 0)
+    queue = (int*)((char*)workspace + ds_bytes(p));
+  FLEXATT_TRY(run_delta(p, o, dout, delta, queue, stream));
+  FLEXATT_TRY(run_dkdv_ds(p, q, k, v, dout, lse, delta, dk, dv, workspace, workspace_bytes, queue, stream));
+  return run_dq_ds(p, k, workspace, workspace_bytes, dq, queue ? queue + 2 : nullptr, stream);
 }
 
 }  // extern "C"

@@ -12,6 +12,7 @@ template <class T>
 __global__ __launch_bounds__(256) void delta_kernel(DeltaArgs a) {
   constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte chunk
   const int tid = threadIdx.x, ln = tid & 15;
+  if (a.zero && blockIdx.x == 0 && tid < 4) a.zero[tid] = 0;  // the next kernels' work queues
   const int64_t row = (int64_t)blockIdx.x * 16 + (tid >> 4);
   const int64_t rows = (int64_t)a.B * a.H * a.S;
   if (row >= rows) return;

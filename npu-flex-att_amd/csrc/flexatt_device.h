@@ -315,6 +315,18 @@ __device__ __forceinline__ int xcd_remap(int w, int n) {
 // groups, and reverses every other run of four, so that the four engines get
 // the same mix of lengths and free their CUs together (longest first within
 // each engine).  False when ng is not a multiple of 8 (caller's own order).
+// Slot (work-item ordinal) of this workgroup: its own index, or, past the
+// first nstatic workgroups (one per CU) when a queue counter is given, the
+// next unclaimed slot, so that workgroups starting early (on faster XCDs)
+// take the longest remaining items.  Every thread of the workgroup calls it.
+__device__ __forceinline__ int queue_slot(int* queue, int nstatic) {
+  if (!queue || (int)blockIdx.x < nstatic) return blockIdx.x;
+  __shared__ int slot;
+  if (threadIdx.x == 0) slot = nstatic + atomicAdd(queue, 1);
+  __syncthreads();
+  return __builtin_amdgcn_readfirstlane(slot);
+}
+
 __device__ __forceinline__ bool xcd_lpt_item(int i, int nk, int ng, int& k, int& g) {
   if ((ng & 7) != 0) return false;
   const int x = i & 7, j = i >> 3;

@@ -19,6 +19,7 @@ struct DeltaArgs {
   View o, dout;
   float* delta;
   int B, H, S, D;
+  int* zero;  // when set: 4 queue counters the pass clears for the kernels after it
 };
 
 struct BwdArgs {
@@ -37,6 +38,10 @@ struct BwdArgs {
   // described with ds_tile_offset); ds == nullptr: not staged.
   char* ds;
   int64_t ds_head;
+  // Work queue (staged path): queue == nullptr keeps the static work order;
+  // otherwise workgroups from nstatic on take their slot from the counter.
+  int* queue;
+  int nstatic;
 };
 
 // Split-KV decode forward (fwd_decode.hip): partials in the caller's workspace.

@@ -35,6 +35,8 @@ EXPORTS = (
 ABI_VERSION = 6
 # Fixed scratch of flexatt_fwd_decode_noalloc (FLEXATT_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = 16 << 20
+# Work-queue counters at the end of the staged-dS workspace (FLEXATT_BWD_QUEUE_BYTES).
+BWD_QUEUE_BYTES = 256
 
 
 class Tensor(ctypes.Structure):

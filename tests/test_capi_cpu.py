@@ -32,6 +32,7 @@ def test_abi_version_and_status_strings():
     lib = L.load()
     assert lib.flexatt_abi_version() == L.ABI_VERSION
     assert f"#define FLEXATT_ABI_VERSION {L.ABI_VERSION}".encode() in open(HEADER, "rb").read()
+    assert f"#define FLEXATT_BWD_QUEUE_BYTES {L.BWD_QUEUE_BYTES}".encode() in open(HEADER, "rb").read()
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.flexatt_status_string(code)
     assert b"head_dim" in lib.flexatt_status_string(-3)
@@ -263,11 +264,12 @@ def _staged_units(sq, skv, causal, window):
 @pytest.mark.parametrize("causal,window", [(0, 0), (1, 0), (1, 1), (1, 100), (0, 33), (1, 128), (1, 2048), (0, 4096)])
 def test_bwd_workspace_counts_the_band(sq, skv, causal, window):
     """flexatt_bwd_workspace (closed form of the staged-dS band) equals the
-    units the dK/dV kernel visits, times B * Hq * 8 KB; 0 off its range."""
+    units the dK/dV kernel visits, times B * Hq * 8 KB, plus the work-queue
+    counters; 0 off its range."""
     lib = L.load()
     p = problem(batch=2, heads_q=6, heads_kv=2, seqlen_q=sq, seqlen_kv=skv, head_dim=128, causal=causal,
                 sliding_window=window)
-    assert lib.flexatt_bwd_workspace(p) == 2 * 6 * _staged_units(sq, skv, causal, window) * 8192
+    assert lib.flexatt_bwd_workspace(p) == 2 * 6 * _staged_units(sq, skv, causal, window) * 8192 + L.BWD_QUEUE_BYTES
 
 
 def test_bwd_workspace_range():
@@ -290,14 +292,15 @@ def test_staged_bwd_rejections():
     t = tens(stride_b=4 * 64 * 128, stride_h=64 * 128, stride_s=128)
     p = problem(head_dim=128)
     need = lib.flexatt_bwd_workspace(p)
-    st = lib.flexatt_bwd_dkdv_ds(p, t, t, t, t, FAKE, FAKE, t, t, FAKE, need - 1, None)
+    band = need - L.BWD_QUEUE_BYTES  # the two kernels on their own need the dS band only
+    st = lib.flexatt_bwd_dkdv_ds(p, t, t, t, t, FAKE, FAKE, t, t, FAKE, band - 1, None)
     assert st == -1
     assert lib.flexatt_bwd_dkdv_ds(p, t, t, t, t, FAKE, FAKE, t, t, None, need, None) == -1
     assert lib.flexatt_bwd_dkdv_ds(p, t, t, t, t, FAKE, FAKE, t, t, FAKE + 8, need, None) == -5
-    assert lib.flexatt_bwd_dq_ds(p, t, FAKE, need - 1, t, None) == -1
+    assert lib.flexatt_bwd_dq_ds(p, t, FAKE, band - 1, t, None) == -1
     assert lib.flexatt_bwd_dq_ds(problem(head_dim=32), tens(), FAKE, need, tens(), None) == -6
     assert lib.flexatt_bwd_dkdv_ds(problem(head_dim=32), tens(), tens(), tens(), tens(), FAKE, FAKE, tens(),
                                    tens(), FAKE, need, None) == -6
-    assert lib.flexatt_bwd_ws(p, t, t, t, t, t, FAKE, FAKE, t, t, t, FAKE, need - 1, None) == -1
+    assert lib.flexatt_bwd_ws(p, t, t, t, t, t, FAKE, FAKE, t, t, t, FAKE, band - 1, None) == -1
     assert lib.flexatt_bwd_ws(p, t, t, t, t, t, FAKE, FAKE, tens(stride_h=0, stride_s=128), t, t, FAKE, need,
                               None) == -5

@@ -100,7 +100,7 @@ def test_staged_ds_values(gpu_device, case):
     L.check(lib.flexatt_bwd_dkdv_ds(p, T(q), T(k), T(v), T(do), lse.data_ptr(), delta.data_ptr(), T(dk), T(dv),
                                     ws.data_ptr(), n, st), "dkdv_ds")
     torch.cuda.synchronize()
-    units = ws.view(dtype).view(-1, 8, 64, 8).cpu().double()  # [unit, fragment, lane, element]
+    units = ws[: n - L.BWD_QUEUE_BYTES].view(dtype).view(-1, 8, 64, 8).cpu().double()  # [unit, fragment, lane, element]
     causal, window = kw.get("causal", False), kw.get("sliding_window", 0)
     nqt, nkb = -(-Sq // 32), -(-Skv // 128)
     # (t, kb) units of one head in storage order
@@ -206,3 +206,52 @@ def test_staged_fully_masked_rows(gpu_device, dtype, d):
     assert (dq[:, :, 131:] == 0).all() and (o[:, :, 131:] == 0).all()
     for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), (o, lse, dq, dk, dv), ref):
         check(name, x, r, dtype)
+
+
+# Grids with more workgroups than CUs: flexatt_bwd_ws hands the workgroups
+# past the first per CU their work items from the queue counters in the
+# workspace (cleared by its Delta pass); the two kernels called on their own
+# keep the static order.  Each item is computed the same way wherever it
+# runs, so the results are bitwise equal, over repeated calls too.
+QUEUE_CASES = {
+    "bf16_d128_causal_gqa4": (torch.bfloat16, 128, 2, 32, 8, 4096, dict(causal=True)),
+    "bf16_d256_window_cap": (torch.bfloat16, 256, 1, 16, 8, 8192, dict(causal=True, sliding_window=4096,
+                                                                       soft_cap=50.0)),
+    "fp16_d64_g7_window": (torch.float16, 64, 2, 28, 4, 8192, dict(causal=True, sliding_window=2048)),
+}
+
+
+@pytest.mark.parametrize("case", list(QUEUE_CASES))
+def test_work_queue_matches_static_order(gpu_device, case):
+    dtype, d, b, hq, hkv, s, kw = QUEUE_CASES[case]
+    g = torch.Generator().manual_seed(21)
+    q, do = (torch.randn(b, hq, s, d, generator=g).to(dtype).cuda() for _ in range(2))
+    k, v = (torch.randn(b, hkv, s, d, generator=g).to(dtype).cuda() for _ in range(2))
+    lib = L.load()
+    p = _problem(q, k, kw)
+    n = lib.flexatt_bwd_workspace(p)
+    assert n > L.BWD_QUEUE_BYTES
+    o, lse = nfa.npu_flash_attention_forward(q, k, v, return_lse=True, **kw)
+    st = torch.cuda.current_stream().cuda_stream
+    T = L.tensor
+
+    def run(whole):
+        delta = torch.empty(b, hq, s, dtype=torch.float32, device=q.device)
+        ws = torch.full((n,), 0x55, dtype=torch.uint8, device=q.device)  # stale counters must not matter
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        if whole:
+            L.check(lib.flexatt_bwd_ws(p, T(q), T(k), T(v), T(o), T(do), lse.data_ptr(), delta.data_ptr(), T(dq),
+                                       T(dk), T(dv), ws.data_ptr(), n, st), "bwd_ws")
+        else:
+            L.check(lib.flexatt_bwd_delta(p, T(o), T(do), delta.data_ptr(), st), "delta")
+            L.check(lib.flexatt_bwd_dkdv_ds(p, T(q), T(k), T(v), T(do), lse.data_ptr(), delta.data_ptr(), T(dk),
+                                            T(dv), ws.data_ptr(), n, st), "dkdv_ds")
+            L.check(lib.flexatt_bwd_dq_ds(p, T(k), ws.data_ptr(), n, T(dq), st), "dq_ds")
+        torch.cuda.synchronize()
+        return dq, dk, dv
+
+    a, b2, c = run(True), run(True), run(False)
+    for name, x, y, z in zip(("dq", "dk", "dv"), a, b2, c):
+        assert bool(torch.isfinite(x).all()), name
+        assert torch.equal(x, y), f"{name}: repeat call differs"
+        assert torch.equal(x, z), f"{name}: queue order differs from the static order"
