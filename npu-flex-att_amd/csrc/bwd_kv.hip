@@ -144,11 +144,17 @@ void bwd_kv_kernel(BwdArgs a) {
   const int qt_lo = q_lo / C::BM;
   const int nqt = q_hi > q_lo ? (q_hi + C::BM - 1) / C::BM - qt_lo : 0;
   const int ntile = p.G * nqt;
-  // Tile order: query tiles from the last one down, the G heads of a query
-  // tile consecutively.  All KV blocks of one (b, hkv) run together on one
-  // XCD and start at the same (last) query tile, so they walk the Q / dO
+  // Tile order: the G heads of a query tile consecutively; the first round
+  // of workgroups (one per CU) walks the query tiles from the last one down,
+  // later ones (causal) from the diagonal up.  The first round starts
+  // together at the last query tile; a later block of b blocks' length ends
+  // when the first round's partner ends, so it starts b time units in and
+  // reaches query tile 4 b + s at time b + s, the same tile for every later
+  // block: in both rounds the KV blocks of one (b, hkv) read the Q / dO
   // stream in step and each tile is fetched from HBM about once.
   const int qt_top = qt_lo + nqt - 1;
+  const bool up = p.causal && slot >= a.nstatic;
+  const int qt0 = up ? qt_lo : qt_top, qt_end = up ? qt_top : qt_lo, qstep = up ? 1 : -1;
 
   // Lane-constant LDS byte offsets of the row reads (S-wave) and the
   // transpose reads (KV-wave) within a tile.
@@ -212,7 +218,7 @@ void bwd_kv_kernel(BwdArgs a) {
     if (p.window > 0) q_hi = min(q_hi, my_kv + p.window + 1);
     if (my_kv >= p.Skv) q_hi = q_lo;
     const unsigned q_w = (unsigned)max(q_hi - q_lo, 0);
-    int cg = 0, cqt = qt_top;  // tile being formed (head, query tile)
+    int cg = 0, cqt = qt0;  // tile being formed (head, query tile)
     int sc = 0;               // its stage
     // Block-sparse maps: the byte of tile u's 128 x 128 block, loaded one
     // step ahead (the S-wave has no other memory operation in flight, so the
@@ -222,7 +228,7 @@ void bwd_kv_kernel(BwdArgs a) {
       return block_row(p, b, hk * p.G + g, min(qt * C::BM, p.Sq - 1))[min(kw0, p.Skv - 1) / kBlk];
     };
     int blk_next = 1;
-    if (p.blk && ntile > 0) blk_next = blk_byte(0, qt_top);
+    if (p.blk && ntile > 0) blk_next = blk_byte(0, qt0);
 
     __syncthreads();  // prologue: tile 0 landed
     for (int u = 0; u <= ntile; ++u) {
@@ -232,7 +238,7 @@ void bwd_kv_kernel(BwdArgs a) {
       bool live = true;
       if (p.blk && act) {
         live = __builtin_amdgcn_readfirstlane(blk_next) != 0;
-        const int ng = cg + 1 == p.G ? 0 : cg + 1, nqt = cg + 1 == p.G ? cqt - 1 : cqt;
+        const int ng = cg + 1 == p.G ? 0 : cg + 1, nqt = cg + 1 == p.G ? cqt + qstep : cqt;
         if (u + 1 < ntile) blk_next = blk_byte(ng, nqt);
       }
       // ---- M(u): S = Q K^T, DP = Delta - dO V^T of tile u; LSE reads ------
@@ -294,7 +300,7 @@ void bwd_kv_kernel(BwdArgs a) {
         const float sl = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
         if (++cg == p.G) {
           cg = 0;
-          --cqt;
+          cqt += qstep;
         }
         sc = sc + 1 == C::STAGES ? 0 : sc + 1;
         // Element r is query row m0 + 8(r/4) + 4h + r%4, KV row my_kv.  Each
@@ -396,17 +402,17 @@ void bwd_kv_kernel(BwdArgs a) {
       crl = min(rl, last);
     };
     // Byte steps: to the next head of the group, and from the last head of a
-    // query tile back to the first head of the query tile below.
+    // query tile back to the first head of the next query tile.
     const int64_t qh = a.q.sh * (int64_t)sizeof(T), oh = a.dout.sh * (int64_t)sizeof(T);
-    const int64_t qback = (int64_t)(p.G - 1) * qh + (int64_t)C::BM * a.q.ss * (int64_t)sizeof(T);
-    const int64_t oback = (int64_t)(p.G - 1) * oh + (int64_t)C::BM * a.dout.ss * (int64_t)sizeof(T);
-    const int64_t lback = (int64_t)(p.G - 1) * p.Sq + C::BM;
-    int is_g = 0, is_qt = qt_top;  // next tile to copy (head, query tile)
+    const int64_t qwrap = (int64_t)qstep * C::BM * a.q.ss * (int64_t)sizeof(T) - (int64_t)(p.G - 1) * qh;
+    const int64_t owrap = (int64_t)qstep * C::BM * a.dout.ss * (int64_t)sizeof(T) - (int64_t)(p.G - 1) * oh;
+    const int64_t lwrap = (int64_t)qstep * C::BM - (int64_t)(p.G - 1) * p.Sq;
+    int is_g = 0, is_qt = qt0;  // next tile to copy (head, query tile)
     const char *qcur, *ocur;
     const float* lcur;  // LSE (lanes 0-7) or Delta (lanes 8-15) row m0
     {
       const int hq = hk * p.G;
-      const int64_t m0 = (int64_t)qt_top * C::BM;
+      const int64_t m0 = (int64_t)qt0 * C::BM;
       qcur = (const char*)((const T*)a.q.data + b * a.q.sb + hq * a.q.sh + m0 * a.q.ss);
       ocur = (const char*)((const T*)a.dout.data + b * a.dout.sb + hq * a.dout.sh + m0 * a.dout.ss);
       lcur = (lane < 8 ? a.lse : a.delta) + (int64_t)(b * p.Hq + hq) * p.Sq + m0;
@@ -432,13 +438,13 @@ void bwd_kv_kernel(BwdArgs a) {
       }
     };
     auto advance = [&]() {  // past the end the last tile is copied again
-      if (is_g < p.G - 1 || is_qt > qt_lo) {
+      if (is_g < p.G - 1 || is_qt != qt_end) {
         if (++is_g == p.G) {
           is_g = 0;
-          --is_qt;
-          qcur -= qback;
-          ocur -= oback;
-          lcur -= lback;
+          is_qt += qstep;
+          qcur += qwrap;
+          ocur += owrap;
+          lcur += lwrap;
           prep();
         } else {
           qcur += qh;
@@ -486,7 +492,7 @@ void bwd_kv_kernel(BwdArgs a) {
     // dsp: this lane's 16 bytes of the unit of (head hk G + ds_g, query tile
     // ds_qt, this KV block), moved per tile with the band counts of the query
     // tiles it passes.
-    int ds_g = 0, ds_qt = qt_top;
+    int ds_g = 0, ds_qt = qt0;
     int xtr = 0;
     char* dsp = nullptr;
     if constexpr (DS) {
@@ -494,7 +500,7 @@ void bwd_kv_kernel(BwdArgs a) {
       const int jr = 4 * (lane >> 5) + ((lane & 15) >> 2);
       xtr = C::XOFF + pr * C::XB + (SLOT_DS + (aq >> 2)) * 1024 + (((aq & 1) << 5) + jr) * 16 + 8 * ((aq >> 1) & 1);
       const int64_t unit = (int64_t)(b * p.Hq + hk * p.G) * a.ds_head +
-                           ds_tile_offset(qt_top, p.causal, p.window, nkb) + kb - ds_kb_lo(qt_top, p.window, nkb);
+                           ds_tile_offset(qt0, p.causal, p.window, nkb) + kb - ds_kb_lo(qt0, p.window, nkb);
       dsp = a.ds + unit * kDsUnitB + (2 * pr) * 1024 + lane * 16;
     }
 
@@ -552,11 +558,13 @@ void bwd_kv_kernel(BwdArgs a) {
                                         (i32x4*)(dsp + f * 1024));
           int64_t step;  // in units
           if (++ds_g == p.G) {
-            // first head, query tile t = ds_qt - 1: the unit index moves by
-            // (offset(t) - kb_lo(t)) - (offset(t + 1) - kb_lo(t + 1)), and
-            // offset(t + 1) - offset(t) = kb_hi(t) - kb_lo(t)
-            const int t = ds_qt - 1;
-            step = ds_kb_lo(ds_qt, p.window, nkb) - ds_kb_hi(t, p.causal, nkb) - (int64_t)(p.G - 1) * a.ds_head;
+            // first head of the next query tile t: the unit index moves by
+            // (offset(t) - kb_lo(t)) - (offset(t') - kb_lo(t')) from tile
+            // t' = ds_qt, and offset(x + 1) - offset(x) = kb_hi(x) - kb_lo(x)
+            const int t = ds_qt + qstep;
+            step = (up ? ds_kb_hi(ds_qt, p.causal, nkb) - ds_kb_lo(t, p.window, nkb)
+                       : ds_kb_lo(ds_qt, p.window, nkb) - ds_kb_hi(t, p.causal, nkb)) -
+                   (int64_t)(p.G - 1) * a.ds_head;
             ds_g = 0;
             ds_qt = t;
           } else {

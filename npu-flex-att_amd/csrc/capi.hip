@@ -255,6 +255,18 @@ BwdLauncher pick_dkdv(const flexatt_problem* p) { return kDkdv[p->dtype][head_in
     if (rc_ != FLEXATT_OK) return rc_; \
   } while (0)
 
+// CUs of the current device (cached per device), 0 if unknown.
+int cu_count() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 int bwd_common(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
                const flexatt_tensor* v, const flexatt_tensor* dout, const float* lse, const float* delta,
                BwdArgs& a) {
@@ -277,7 +289,7 @@ int bwd_common(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_
   a.ds = nullptr;
   a.ds_head = 0;
   a.queue = nullptr;
-  a.nstatic = 0;
+  a.nstatic = cu_count() & ~7;  // the first round of workgroups (also sets the dK/dV walk direction)
   return FLEXATT_OK;
 }
 
@@ -310,18 +322,6 @@ size_t ds_bytes(const flexatt_problem* p) {
   if (!ds_applies(p)) return 0;
   return (size_t)((int64_t)p->batch * p->heads_q * ds_units_per_head(p) * kDsUnitB);
 }
-// CUs of the current device (cached per device), 0 if unknown.
-int cu_count() {
-  static int cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cache[dev] = n;
-  }
-  return cache[dev];
-}
-
 int ds_workspace(const flexatt_problem* p, void* ws, size_t bytes, BwdArgs& a) {
   if (!ds_applies(p)) return FLEXATT_ERANGE;
   if (!ws) return FLEXATT_EINVAL;
