@@ -520,8 +520,12 @@ void fwd_mfma_kernel(FwdArgs a) {
         wait_tile();
         __syncthreads();
         pin_p();
+        // the MFMA phase issues ahead of the other wave's softmax on the SIMD
+        // (measured 1-1.5% faster; raising the softmax wave instead is slower)
+        __builtin_amdgcn_s_setprio(1);
         issue_next();  // t + 3
         mphase((t - t_lo) & 3, (t + 1 - t_lo) & 3, true, true);
+        __builtin_amdgcn_s_setprio(0);
         wait_tile();
         __syncthreads();
         pin_s();
