@@ -33,8 +33,8 @@
 //            P (dP - Delta) is one multiply);  KV-wave: reads the packed
 //            P / dS of tile u-1 and the first transpose reads;
 //      V(u): S-wave: P / dS of tile u (VALU), written to the exchange buffer;
-//            KV-wave: the 16 dV / dK MFMAs of tile u-1, then waits for tile
-//            u+1;
+//            KV-wave: the 16 dV / dK MFMAs of tile u-1, the staged dS stores
+//            of tile u-1 (when staged), then waits for tile u+1;
 //    so that each SIMD alternates between the S-wave's MFMAs and the
 //    KV-wave's MFMAs beside the S-wave's VALU work.  The KV-wave issues the
 //    copies of tile u+4 in M(u): a global -> LDS copy holds its wave for
@@ -513,6 +513,34 @@ void bwd_kv_kernel(BwdArgs a) {
       }
       wait_vmcnt<(C::AHEAD - 1) * CNT>();
     }
+    // Staged dS of tile u-1 (st4, read from the exchange buffer in M(u)) to
+    // its unit, and the unit cursor to the next tile.  Issued in V(u) after the
+    // MFMAs at D = 128 and 256, where the KV-wave waits for the S-wave's VALU
+    // work anyway (3% faster there), in M(u) at D = 64 (3% faster there); the
+    // tile waits count the stores either way, as they precede them.
+    constexpr bool DS_LATE = D != 64;
+    auto store_ds = [&](const i16x4 (&st4)[4]) {
+      // streamed past the caches: each fragment is read once, by the dQ kernel
+#pragma unroll
+      for (int f = 0; f < 2; ++f)
+        __builtin_nontemporal_store(__builtin_bit_cast(i32x4, cat_tr<V8>(st4[2 * f], st4[2 * f + 1])),
+                                    (i32x4*)(dsp + f * 1024));
+      int64_t step;  // in units
+      if (++ds_g == p.G) {
+        // first head of the next query tile t: the unit index moves by
+        // (offset(t) - kb_lo(t)) - (offset(t') - kb_lo(t')) from tile
+        // t' = ds_qt, and offset(x + 1) - offset(x) = kb_hi(x) - kb_lo(x)
+        const int t = ds_qt + qstep;
+        step = (up ? ds_kb_hi(ds_qt, p.causal, nkb) - ds_kb_lo(t, p.window, nkb)
+                   : ds_kb_lo(ds_qt, p.window, nkb) - ds_kb_hi(t, p.causal, nkb)) -
+               (int64_t)(p.G - 1) * a.ds_head;
+        ds_g = 0;
+        ds_qt = t;
+      } else {
+        step = a.ds_head;
+      }
+      dsp += step * kDsUnitB;
+    };
     __syncthreads();  // prologue
     for (int u = 0; u <= ntile; ++u) {
       const bool act = u > 0;
@@ -521,6 +549,7 @@ void bwd_kv_kernel(BwdArgs a) {
       //      phase), packed P / dS of tile u-1, first transpose reads --------
       V8 PP[2], PS[2];
       i16x4 blo[RAK + 1], bhi[RAK + 1];
+      i16x4 st4[4];  // staged dS of tile u-1: read in M(u), stored in V(u)
       if (ntile > 0) {
 #pragma unroll
         for (int j = 0; j < CNT; ++j) copy_op(s_cp, j);
@@ -539,7 +568,6 @@ void bwd_kv_kernel(BwdArgs a) {
           PS[0] = *(const V8*)xslot(u - 1, SLOT_DS);
           PS[1] = *(const V8*)xslot(u - 1, SLOT_DS + 1);
         }
-        i16x4 st4[4];
         if constexpr (DS) {
           const char* xb = smem + xtr + ((u - 1) & 1) * (C::NP * C::XB);
 #pragma unroll
@@ -550,28 +578,7 @@ void bwd_kv_kernel(BwdArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < RAK; ++j) rdB(j, blo[j], bhi[j]);
-        if constexpr (DS) {
-          // streamed past the caches: each fragment is read once, by the dQ kernel
-#pragma unroll
-          for (int f = 0; f < 2; ++f)
-            __builtin_nontemporal_store(__builtin_bit_cast(i32x4, cat_tr<V8>(st4[2 * f], st4[2 * f + 1])),
-                                        (i32x4*)(dsp + f * 1024));
-          int64_t step;  // in units
-          if (++ds_g == p.G) {
-            // first head of the next query tile t: the unit index moves by
-            // (offset(t) - kb_lo(t)) - (offset(t') - kb_lo(t')) from tile
-            // t' = ds_qt, and offset(x + 1) - offset(x) = kb_hi(x) - kb_lo(x)
-            const int t = ds_qt + qstep;
-            step = (up ? ds_kb_hi(ds_qt, p.causal, nkb) - ds_kb_lo(t, p.window, nkb)
-                       : ds_kb_lo(ds_qt, p.window, nkb) - ds_kb_hi(t, p.causal, nkb)) -
-                   (int64_t)(p.G - 1) * a.ds_head;
-            ds_g = 0;
-            ds_qt = t;
-          } else {
-            step = a.ds_head;
-          }
-          dsp += step * kDsUnitB;
-        }
+        if constexpr (DS && !DS_LATE) store_ds(st4);
       }
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();  // X(u)
@@ -590,6 +597,7 @@ void bwd_kv_kernel(BwdArgs a) {
           else dv[db] = M::mma(av, PP[qc], dv[db]);
         }
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (DS && DS_LATE) store_ds(st4);
         s_tr = s_tr + 1 == C::STAGES ? 0 : s_tr + 1;
       }
       if (ntile > 0) {
