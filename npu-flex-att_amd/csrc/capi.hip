@@ -126,19 +126,20 @@ Shape make_shape(const flexatt_problem* p) {
 View view(const flexatt_tensor* t) { return View{t->data, t->stride_b, t->stride_h, t->stride_s}; }
 MutView mview(const flexatt_tensor* t) { return MutView{t->data, t->stride_b, t->stride_h, t->stride_s}; }
 
-// [dtype][head index]
+// [dtype][head index]; fp32 on the fp32 matrix cores except the D = 256
+// backward (vector ALU kernels)
 const FwdLauncher kFwd[3][4] = {
-    {fwd_simt_f32_d32, fwd_simt_f32_d64, fwd_simt_f32_d128, fwd_simt_f32_d256},
+    {fwd_f32_d32, fwd_f32_d64, fwd_f32_d128, fwd_f32_d256},
     {fwd_mfma_f16_d32, fwd_mfma_f16_d64, fwd_mfma_f16_d128, fwd_mfma_f16_d256},
     {fwd_mfma_bf16_d32, fwd_mfma_bf16_d64, fwd_mfma_bf16_d128, fwd_mfma_bf16_d256},
 };
 const BwdLauncher kDq[3][4] = {
-    {bwd_dq_simt_f32_d32, bwd_dq_simt_f32_d64, bwd_dq_simt_f32_d128, bwd_dq_simt_f32_d256},
+    {bwd_dq_f32_d32, bwd_dq_f32_d64, bwd_dq_f32_d128, bwd_dq_simt_f32_d256},
     {bwd_dq_mfma_f16_d32, bwd_dq_mfma_f16_d64, bwd_q_f16_d128, bwd_dq_mfma_f16_d256},
     {bwd_dq_mfma_bf16_d32, bwd_dq_mfma_bf16_d64, bwd_q_bf16_d128, bwd_dq_mfma_bf16_d256},
 };
 const BwdLauncher kDkdv[3][4] = {
-    {bwd_dkdv_simt_f32_d32, bwd_dkdv_simt_f32_d64, bwd_dkdv_simt_f32_d128, bwd_dkdv_simt_f32_d256},
+    {bwd_dkdv_f32_d32, bwd_dkdv_f32_d64, bwd_dkdv_f32_d128, bwd_dkdv_simt_f32_d256},
     {bwd_dkdv_mfma_f16_d32, bwd_kv_f16_d64, bwd_kv_f16_d128, bwd_kv_f16_d256},
     {bwd_dkdv_mfma_bf16_d32, bwd_kv_bf16_d64, bwd_kv_bf16_d128, bwd_kv_bf16_d256},
 };

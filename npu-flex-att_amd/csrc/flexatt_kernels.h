@@ -67,10 +67,7 @@ typedef hipError_t (*BwdLauncher)(const BwdArgs&, hipStream_t);
   hipError_t bwd_dq_mfma_bf16_d##D(const BwdArgs&, hipStream_t);              \
   hipError_t bwd_dq_mfma_f16_d##D(const BwdArgs&, hipStream_t);               \
   hipError_t bwd_dkdv_mfma_bf16_d##D(const BwdArgs&, hipStream_t);            \
-  hipError_t bwd_dkdv_mfma_f16_d##D(const BwdArgs&, hipStream_t);             \
-  hipError_t fwd_simt_f32_d##D(const FwdArgs&, hipStream_t);                  \
-  hipError_t bwd_dq_simt_f32_d##D(const BwdArgs&, hipStream_t);               \
-  hipError_t bwd_dkdv_simt_f32_d##D(const BwdArgs&, hipStream_t);
+  hipError_t bwd_dkdv_mfma_f16_d##D(const BwdArgs&, hipStream_t);
 
 FLEXATT_DECL_D(32)
 FLEXATT_DECL_D(64)
@@ -110,6 +107,21 @@ hipError_t bwd_kv_ds_bf16_d256(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_ds_f16_d256(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_bf16_d256(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_f16_d256(const BwdArgs&, hipStream_t);
+
+// fp32 inputs on the fp32 matrix cores (f32_mfma.hip): forward at every D,
+// dQ and dK/dV at D <= 128; the D = 256 backward on the vector ALUs (simt.hip).
+hipError_t fwd_f32_d32(const FwdArgs&, hipStream_t);
+hipError_t fwd_f32_d64(const FwdArgs&, hipStream_t);
+hipError_t fwd_f32_d128(const FwdArgs&, hipStream_t);
+hipError_t fwd_f32_d256(const FwdArgs&, hipStream_t);
+hipError_t bwd_dq_f32_d32(const BwdArgs&, hipStream_t);
+hipError_t bwd_dq_f32_d64(const BwdArgs&, hipStream_t);
+hipError_t bwd_dq_f32_d128(const BwdArgs&, hipStream_t);
+hipError_t bwd_dkdv_f32_d32(const BwdArgs&, hipStream_t);
+hipError_t bwd_dkdv_f32_d64(const BwdArgs&, hipStream_t);
+hipError_t bwd_dkdv_f32_d128(const BwdArgs&, hipStream_t);
+hipError_t bwd_dq_simt_f32_d256(const BwdArgs&, hipStream_t);
+hipError_t bwd_dkdv_simt_f32_d256(const BwdArgs&, hipStream_t);
 
 // dQ as a query-stationary tile stream (bwd_q.hip), D = 128; with
 // a.delta_out set it also computes Delta (written there) from O and dO.

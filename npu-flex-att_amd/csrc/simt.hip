@@ -1,12 +1,14 @@
-// fp32 flash attention (forward, dQ, dK/dV) on the vector ALUs.
+// fp32 flash-attention backward (dQ, dK/dV) on the vector ALUs.
 //
-// The reference accepts fp32 tensors on the same entry points
+// The library's fp32 path runs on the fp32 matrix cores (f32_mfma.hip); these
+// kernels serve the fp32 backward at head_dim 256, whose dK/dV would need K,
+// V, dK and dV of a 32-row block resident per lane (512 values) on the
+// matrix cores.  The reference accepts fp32 tensors on the same entry points
 // (test/test_supplementary.py:55-63; the fp32 suites of
 // test/test_comprehensive.py) and expects fp32-exact results (tolerances down
-// to 1e-5, test/test_comprehensive.py:88).  gfx950 has no reduced-precision
-// fp32 MFMA, so the fp32 path computes exactly in fp32 FMA: one 16-lane group
-// per row, K/V (or Q/dO) tiles staged in LDS, online softmax in the natural
-// domain with expf/logf/tanhf.  Semantics are those of the MFMA kernels
+// to 1e-5, test/test_comprehensive.py:88): one 16-lane group per row, K/V (or
+// Q/dO) tiles staged in LDS, fp32 FMA, online softmax in the natural domain
+// with expf/logf/tanhf.  Semantics are those of the MFMA kernels
 // (npu_flash_attention.py:17-166, :298-402, :407-560), including the KV tail,
 // ALiBi in backward and the in-kernel GQA group sum.
 #include "flexatt_device.h"
@@ -42,89 +44,6 @@ __device__ __forceinline__ float score(float s, const Shape& p, float slope, int
   return x;
 }
 }  // namespace simt
-
-template <int D>
-__global__ __launch_bounds__(256) void fwd_simt_kernel(FwdArgs a) {
-  using namespace simt;
-  constexpr int E = D / kLanes;
-  __shared__ float sK[kTile][D];
-  __shared__ float sV[kTile][D];
-  const Shape& p = a.p;
-  const int tid = threadIdx.x, rg = tid / kLanes, ln = tid % kLanes;
-  const int qt = blockIdx.x % a.nqt, bh = blockIdx.x / a.nqt;
-  const int hq = bh % p.Hq, b = bh / p.Hq, hk = hq / p.G;
-  const int m0 = qt * kRows, my_m = m0 + rg;
-  const float* qp = (const float*)a.q.data + b * a.q.sb + hq * a.q.sh;
-  const float* kp = (const float*)a.k.data + b * a.k.sb + hk * a.k.sh;
-  const float* vp = (const float*)a.v.data + b * a.v.sb + hk * a.v.sh;
-  float q[E], acc[E];
-  const int rq = min(my_m, p.Sq - 1);
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    q[e] = my_m < p.Sq ? qp[(int64_t)rq * a.q.ss + ln + kLanes * e] : 0.f;
-    acc[e] = 0.f;
-  }
-  const float slope = p.alibi ? p.alibi[hq] : 0.f;
-  int kv_lo = 0, kv_hi = p.Skv;
-  if (p.causal) kv_hi = min(kv_hi, m0 + kRows);
-  if (p.window > 0) kv_lo = max(0, m0 - p.window);
-  int dlo, dhi;
-  doc_bounds(p, b, rq, dlo, dhi);
-  if (p.doc) {  // KV range of the block's documents
-    int l0, h0, l1, h1;
-    doc_bounds(p, b, min(m0, p.Sq - 1), l0, h0);
-    doc_bounds(p, b, min(m0 + kRows, p.Sq) - 1, l1, h1);
-    kv_lo = max(kv_lo, l0);
-    kv_hi = min(kv_hi, h1);
-  }
-  float m_run = kNegInf, l_run = 0.f;
-  for (int n0 = (kv_lo / kTile) * kTile; n0 < kv_hi; n0 += kTile) {
-    __syncthreads();
-    for (int idx = tid; idx < kTile * D; idx += 256) {
-      const int r = idx / D, c = idx % D, n = n0 + r;
-      const int nc = min(n, p.Skv - 1);
-      sK[r][c] = n < p.Skv ? kp[(int64_t)nc * a.k.ss + c] : 0.f;
-      sV[r][c] = n < p.Skv ? vp[(int64_t)nc * a.v.ss + c] : 0.f;
-    }
-    __syncthreads();
-    float sc[kTile];
-    float mx = kNegInf;
-#pragma unroll
-    for (int jj = 0; jj < kTile; ++jj) {
-      float part = 0.f;
-#pragma unroll
-      for (int e = 0; e < E; ++e) part = fmaf(q[e], sK[jj][ln + kLanes * e], part);
-      part = group_sum(part);
-      const int j = n0 + jj;
-      float t;
-      float x = score(part, p, slope, my_m, j, t);
-      if (!allowed(p, my_m, j) || j < dlo || j >= dhi || !block_on(p, b, hq, min(my_m, p.Sq - 1), j)) x = kNegInf;
-      sc[jj] = x;
-      mx = fmaxf(mx, x);
-    }
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == kNegInf ? 0.f : m_new;
-    const float alpha = expf(m_run - m_use);
-    l_run *= alpha;
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] *= alpha;
-#pragma unroll
-    for (int jj = 0; jj < kTile; ++jj) {
-      const float pj = expf(sc[jj] - m_use);
-      l_run += pj;
-#pragma unroll
-      for (int e = 0; e < E; ++e) acc[e] = fmaf(pj, sV[jj][ln + kLanes * e], acc[e]);
-    }
-    m_run = m_new;
-  }
-  if (my_m < p.Sq) {
-    const bool empty = !(l_run > 0.f);
-    float* op = (float*)a.o.data + b * a.o.sb + hq * a.o.sh + (int64_t)my_m * a.o.ss;
-#pragma unroll
-    for (int e = 0; e < E; ++e) op[ln + kLanes * e] = empty ? 0.f : acc[e] / l_run;
-    if (ln == 0) a.lse[(int64_t)(b * p.Hq + hq) * p.Sq + my_m] = empty ? kNegInf : m_run + logf(l_run);
-  }
-}
 
 template <int D>
 __global__ __launch_bounds__(256) void bwd_dq_simt_kernel(BwdArgs a) {
@@ -303,12 +222,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_simt_kernel(BwdArgs a) {
 
 #define FLEXATT_CAT2(a, b) a##b
 #define FLEXATT_CAT(a, b) FLEXATT_CAT2(a, b)
-hipError_t FLEXATT_CAT(fwd_simt_f32_d, FLEXATT_D)(const FwdArgs& a, hipStream_t st) {
-  FwdArgs x = a;
-  x.nqt = (a.p.Sq + simt::kRows - 1) / simt::kRows;
-  hipLaunchKernelGGL((fwd_simt_kernel<FLEXATT_D>), dim3(x.nqt * a.p.B * a.p.Hq), dim3(256), 0, st, x);
-  return hipGetLastError();
-}
+#if FLEXATT_D == 256
 hipError_t FLEXATT_CAT(bwd_dq_simt_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
   BwdArgs x = a;
   x.ntiles = (a.p.Sq + simt::kRows - 1) / simt::kRows;
@@ -321,5 +235,7 @@ hipError_t FLEXATT_CAT(bwd_dkdv_simt_f32_d, FLEXATT_D)(const BwdArgs& a, hipStre
   hipLaunchKernelGGL((bwd_dkdv_simt_kernel<FLEXATT_D>), dim3(x.ntiles * a.p.B * a.p.Hkv), dim3(256), 0, st, x);
   return hipGetLastError();
 }
+
+#endif
 
 }  // namespace flexatt
