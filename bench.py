@@ -32,10 +32,14 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "npu-flex-att_amd"))
 
 PEAK_TFLOPS = 2516.6  # dense bf16/fp16 MFMA
+PEAK_BY_DTYPE = {"bf16": PEAK_TFLOPS, "fp16": PEAK_TFLOPS, "fp32": 157.3}  # dense MFMA per input dtype
+TORCH_DTYPE = {"bf16": "bfloat16", "fp16": "float16", "fp32": "float32"}
 
 CONFIGS = {
     # name: (B, Hq, Hkv, Sq, Skv, D, dtype, causal, window, soft_cap, alibi, scale, input_scale)
     "gqa_llama3_8b": (2, 32, 8, 4096, 4096, 128, "bf16", True, 0, 0.0, False, None, 1.0),
+    # the same shape on the fp32 path (fp32 matrix cores; peak 157.3 TFLOP/s)
+    "gqa_llama3_8b_fp32": (2, 32, 8, 4096, 4096, 128, "fp32", True, 0, 0.0, False, None, 1.0),
     "gemma2_d256": (1, 16, 8, 8192, 8192, 256, "bf16", True, 4096, 50.0, False, 1.0 / 16, 2.0),
     "all_primitives_d64": (1, 28, 4, 16384, 16383, 64, "fp16", True, 2048, 30.0, True, 0.05, 1.0),
     # the reference's own perf-table shapes (RESULT.md:163-167)
@@ -65,7 +69,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bounded CPU baseline sample budget")
     ap.add_argument("--layout", default="bnsd", choices=("bnsd", "bsnd"),
                     help="storage of Q/K/V/dO (and so O, dQ, dK, dV): [B,H,S,D], or [B,S,H,D] passed as strided views")
-    ap.add_argument("--no-gemm-peak", action="store_true", help="skip the plain bf16 GEMM reference rate")
+    ap.add_argument("--no-gemm-peak", action="store_true", help="skip the plain GEMM reference rate")
     ap.add_argument("--recompute-dq", action="store_true",
                     help="backward without dS staging: the dQ kernel recomputes S and dP (flexatt_bwd)")
     ap.add_argument("--block-sparsity", type=float, default=0.0,
@@ -127,7 +131,8 @@ def main():
         return decode_main(args, dev)
     nfa.ds_staging_enabled = not args.recompute_dq
     B, Hq, Hkv, Sq, Skv, D, dts, causal, window, cap, alibi, scale, insc = CONFIGS[args.config]
-    dtype = {"bf16": torch.bfloat16, "fp16": torch.float16}[dts]
+    dtype = getattr(torch, TORCH_DTYPE[dts])
+    peak = PEAK_BY_DTYPE[dts]
     g = torch.Generator().manual_seed(42)
     q = (torch.randn(B, Hq, Sq, D, generator=g) * insc).to(dtype).to(dev)
     k = (torch.randn(B, Hkv, Skv, D, generator=g) * insc).to(dtype).to(dev)
@@ -238,7 +243,7 @@ def main():
     dom = max(per_kernel_flop, key=lambda n: kernel_ms[n])
     achieved = per_kernel_flop[dom] / kernel_ms[dom] / 1e9
 
-    gemm = None if args.no_gemm_peak else gemm_peak(dev)
+    gemm = None if args.no_gemm_peak else gemm_peak(dev, dtype, dts)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -269,16 +274,16 @@ def main():
         "kernel_ms": {k_: round(v_, 4) for k_, v_ in kernel_ms.items()},
         "fwd_tflops": round(fwd_tf, 1),
         "bwd_tflops": round(bwd_tf, 1),
-        "fwd_frac_peak": round(fwd_tf / PEAK_TFLOPS, 4),
-        "bwd_frac_peak": round(bwd_tf / PEAK_TFLOPS, 4),
-        "frac_peak": round(total_tf / PEAK_TFLOPS, 4),
+        "fwd_frac_peak": round(fwd_tf / peak, 4),
+        "bwd_frac_peak": round(bwd_tf / peak, 4),
+        "frac_peak": round(total_tf / peak, 4),
         "roofline": {
             "kernel": dom,
             "bound": "mfma",
             "achieved": round(achieved, 1),
-            "peak": PEAK_TFLOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_TFLOPS, 4),
+            "frac": round(achieved / peak, 4),
             "traffic": recorded_traffic(args.config, dom) if masks is None else None,
         },
         "cpu_baseline": cpu,
@@ -383,13 +388,13 @@ def decode_main(args, dev):
     print(json.dumps(out), flush=True)
 
 
-def gemm_peak(dev):
-    """Plain bf16 GEMM rate (torch.matmul, i.e. hipBLASLt): 8192^3, median of 20."""
+def gemm_peak(dev, dtype, name):
+    """Plain GEMM rate in the workload's dtype (torch.matmul, i.e. hipBLASLt): 8192^3, median of 20."""
     import torch
 
     n = 8192
-    a = torch.randn(n, n, device=dev).to(torch.bfloat16)
-    b = torch.randn(n, n, device=dev).to(torch.bfloat16)
+    a = torch.randn(n, n, device=dev).to(dtype)
+    b = torch.randn(n, n, device=dev).to(dtype)
     for _ in range(3):
         torch.matmul(a, b)
     st = torch.cuda.current_stream(dev)
@@ -400,7 +405,7 @@ def gemm_peak(dev):
         e1.record(st)
     torch.cuda.synchronize()
     ms = statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
-    return {"tflops": round(2.0 * n ** 3 / ms / 1e9, 1), "shape": f"{n}x{n}x{n} bf16 torch.matmul"}
+    return {"tflops": round(2.0 * n ** 3 / ms / 1e9, 1), "shape": f"{n}x{n}x{n} {name} torch.matmul"}
 
 
 def cpu_baseline(q, k, v, do, kw, slopes, budget_s, G, causal, window, D, Sq, Skv):
