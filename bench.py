@@ -75,6 +75,9 @@ def parse():
     ap.add_argument("--block-sparsity", type=float, default=0.0,
                     help="also pass a block-sparse map (128 x 128 blocks, shared by all heads) with this fraction "
                          "of the off-diagonal blocks removed; FLOPs count the remaining pairs")
+    ap.add_argument("--graph", action="store_true",
+                    help="time replays of the step captured once as a HIP graph (torch.cuda.graph) instead of "
+                         "eager API calls")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one 256 MiB device copy (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -182,9 +185,21 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    run = step
+    if args.graph:
+        # the whole step (forward + backward, its allocations from the graph's
+        # pool) captured once; each timed step is one replay
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        run = graph.replay
+        for _ in range(args.warmup):
+            run()
+        torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        run()
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
@@ -262,6 +277,7 @@ def main():
         "vs_baseline": None,
         "dtype": dts,
         "data": "synthetic N(0,1), seed 42, resident in HBM",
+        "step_launch": "hip graph replay" if args.graph else "eager API calls",
         "config": {
             "workload": f"{args.config}: {dts} B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} Skv={Skv} D={D} causal={causal} "
                         f"window={window} soft_cap={cap} alibi={alibi} scale={scale}"

@@ -74,13 +74,46 @@ def test_golden_combos_fp32(gpu_device, gold, name):
         check(nm, x, torch.from_numpy(gold[f"{name}/{nm}"]), torch.float32)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "fp16", "fp32"])
 @pytest.mark.parametrize("sq,skv", [(1, 1), (16, 16), (33, 33), (65, 47), (47, 300), (300, 47), (129, 127)])
 def test_ragged_lengths(gpu_device, dtype, sq, skv):
     cpu, dev = draw(5, 1, 2, 1, sq, skv, 64, dtype)
     for causal, window in ((True, 0), (False, 0), (True, 9), (False, 9)):
         got = fwd_bwd(nfa, *dev, causal=causal, sliding_window=window)
         ref = oracle_fwd_bwd(*cpu, causal=causal, sliding_window=window)
+        for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
+            check(name, x, r, dtype)
+
+
+@pytest.mark.parametrize("flags", ["full", "causal", "causal_window", "window"])
+@pytest.mark.parametrize("d", HEAD_DIMS)
+def test_fp32_several_tiles(gpu_device, d, flags):
+    # fp32 matrix-core kernels over several work items per head (the forward
+    # takes 256 query rows per workgroup, dQ and dK/dV 128 or 256 rows), G = 3,
+    # Sq != Skv, lengths off the tile grid.
+    causal, window, alibi, cap, scale = FLAGS[flags]
+    window = 90 if window else 0
+    cpu, dev = draw(17, 1, 6, 2, 600, 563, d, torch.float32)
+    kw = dict(causal=causal, sliding_window=window, scale=scale)
+    got = fwd_bwd(nfa, *dev, **kw)
+    ref = oracle_fwd_bwd(*cpu, causal=causal, sliding_window=window, scale=scale)
+    for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
+        check(name, x, r, torch.float32)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "fp16", "fp32"])
+def test_relative_position_score_mod(gpu_device, dtype):
+    # FlexAttention's relative-position score_mod, score + (q_idx - kv_idx),
+    # is ALiBi with slope 1 in this API's sign convention (+slope * (i - j)).
+    # 96 positions: the bias reaches 95, where an fp32 score carries a rounding
+    # error of half an ulp (3.8e-6) -- any fp32 softmax over scores of a few
+    # hundred exceeds the 1e-5 bound on O by its input rounding alone.
+    hq = 4
+    cpu, dev = draw(23, 1, hq, 2, 96, 96, 64, dtype)
+    ones = torch.ones(hq, dtype=torch.float32)
+    for causal, window in ((True, 0), (False, 0), (True, 20)):
+        got = fwd_bwd(nfa, *dev, causal=causal, sliding_window=window, scale=0.1, alibi_slope=ones.to(gpu_device))
+        ref = oracle_fwd_bwd(*cpu, causal=causal, sliding_window=window, scale=0.1, alibi_slope=ones)
         for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
             check(name, x, r, dtype)
 
