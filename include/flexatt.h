@@ -179,12 +179,14 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
 /* Bytes of work-queue counters at the end of the staged-dS workspace. */
 #define FLEXATT_BWD_QUEUE_BYTES 256
 
-/* Backward with dS staged through HBM (fp16/bf16, head_dim 64, 128 or 256).  The dK/dV kernel already forms dS for every attended
- * pair; it writes those values (rounded to the input dtype, as its own dK
- * MFMAs consume them) to a caller-owned workspace, and the dQ kernel forms
- * dQ = scale * dS K from them instead of recomputing S and dP.  The
- * workspace holds 2 bytes per attended (query row, KV row) pair of each
- * query head, in 32 x 128 units over the causal / window band (interval
+/* Backward with dS staged through HBM (fp16/bf16 at head_dim 64, 128 or
+ * 256; fp32 at head_dim 32, 64 or 128).  The dK/dV kernel already forms dS
+ * for every attended pair; it writes those values (rounded to the input
+ * dtype, as its own dK MFMAs consume them) to a caller-owned workspace, and
+ * the dQ kernel forms dQ = scale * dS K from them instead of recomputing S
+ * and dP.  The workspace holds 2 bytes (fp32: 4 bytes) per attended (query
+ * row, KV row) pair of each query head, in 32 x 128 units over the causal /
+ * window band (interval
  * and block masks keep that band; their masked pairs hold zeros),
  * followed by FLEXATT_BWD_QUEUE_BYTES of work-queue counters:
  * flexatt_bwd_workspace(p) bytes in all (0: the problem is outside this
@@ -197,8 +199,9 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
  * npu_flash_attention.py:681-737): the Delta pass into `delta`, dK/dV
  * writing dS, then dQ.  Past the first workgroup per CU, the dK/dV and dQ
  * workgroups take the longest remaining work items from the queue counters
- * (which the Delta pass clears), so that faster XCDs take more work; with a
- * workspace of only the dS band's size the static order is kept.  Outside
+ * (which the Delta pass clears), so that faster XCDs take more work (fp16/
+ * bf16); with a workspace of only the dS band's size the static order is
+ * kept.  Outside
  * the range it runs flexatt_bwd and the workspace may be NULL. */
 size_t flexatt_bwd_workspace(const flexatt_problem* p);
 int flexatt_bwd_ws(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,

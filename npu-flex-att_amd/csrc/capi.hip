@@ -294,21 +294,27 @@ int bwd_common(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_
   return FLEXATT_OK;
 }
 
-// Staged dS (D = 64, 128 and 256, fp16/bf16, every mask primitive: the
-// dK/dV kernel masks per element and stores every unit of the causal /
-// window band, zero where masked): units per query head and workspace
-// bytes; 0 when the problem takes the recomputing dQ kernel.
+// Staged dS (fp16/bf16 at D = 64, 128 and 256; fp32 at D = 32, 64 and 128;
+// every mask primitive: the dK/dV kernel masks per element and stores every
+// unit of the causal / window band, zero where masked): units per query head
+// and workspace bytes; 0 when the problem takes the recomputing dQ kernel.
 bool ds_applies(const flexatt_problem* p) {
+  if (p->dtype == FLEXATT_F32) return p->head_dim <= 128;
   return (p->dtype == FLEXATT_F16 || p->dtype == FLEXATT_BF16) &&
          (p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256);
 }
+int64_t ds_unit_bytes(const flexatt_problem* p) { return p->dtype == FLEXATT_F32 ? kDsUnitB32 : kDsUnitB; }
 BwdLauncher pick_kv_ds(const flexatt_problem* p) {
+  if (p->dtype == FLEXATT_F32)
+    return p->head_dim == 32 ? bwd_kv_ds_f32_d32 : (p->head_dim == 64 ? bwd_kv_ds_f32_d64 : bwd_kv_ds_f32_d128);
   const bool bf = p->dtype == FLEXATT_BF16;
   if (p->head_dim == 64) return bf ? bwd_kv_ds_bf16_d64 : bwd_kv_ds_f16_d64;
   if (p->head_dim == 256) return bf ? bwd_kv_ds_bf16_d256 : bwd_kv_ds_f16_d256;
   return bf ? bwd_kv_ds_bf16_d128 : bwd_kv_ds_f16_d128;
 }
 BwdLauncher pick_dq_ds(const flexatt_problem* p) {
+  if (p->dtype == FLEXATT_F32)
+    return p->head_dim == 32 ? bwd_dq_ds_f32_d32 : (p->head_dim == 64 ? bwd_dq_ds_f32_d64 : bwd_dq_ds_f32_d128);
   const bool bf = p->dtype == FLEXATT_BF16;
   if (p->head_dim == 64) return bf ? bwd_dq_ds_bf16_d64 : bwd_dq_ds_f16_d64;
   if (p->head_dim == 256) return bf ? bwd_dq_ds_bf16_d256 : bwd_dq_ds_f16_d256;
@@ -321,7 +327,7 @@ int64_t ds_units_per_head(const flexatt_problem* p) {
 }
 size_t ds_bytes(const flexatt_problem* p) {
   if (!ds_applies(p)) return 0;
-  return (size_t)((int64_t)p->batch * p->heads_q * ds_units_per_head(p) * kDsUnitB);
+  return (size_t)((int64_t)p->batch * p->heads_q * ds_units_per_head(p) * ds_unit_bytes(p));
 }
 int ds_workspace(const flexatt_problem* p, void* ws, size_t bytes, BwdArgs& a) {
   if (!ds_applies(p)) return FLEXATT_ERANGE;

@@ -529,7 +529,7 @@ struct F32Kv {
   static constexpr int BN = 32 * NW;  // KV rows per workgroup
 };
 
-template <int D, bool SOFTCAP, bool ALIBI>
+template <int D, bool SOFTCAP, bool ALIBI, bool DS>
 __global__ __launch_bounds__(F32Kv<D>::NW * 64) __attribute__((amdgpu_waves_per_eu(F32Kv<D>::WPE, F32Kv<D>::WPE)))
 void bwd_dkdv_f32_kernel(BwdArgs a) {
   using namespace f32m;
@@ -580,10 +580,12 @@ void bwd_dkdv_f32_kernel(BwdArgs a) {
   if (p.window > 0) w_hi = min(w_hi, nlast + p.window + 1);
   if (p.docc) {
     int l0, h0, l1, h1;
-    col_bounds(p, b, min(n0, p.Skv - 1), l0, h0);
-    col_bounds(p, b, min(n0 + BN, p.Skv) - 1, l1, h1);
-    q_lo = max(q_lo, l0);
-    q_hi = min(q_hi, h1);
+    if constexpr (!DS) {  // DS: every query tile of the causal / window band is visited (and its dS stored)
+      col_bounds(p, b, min(n0, p.Skv - 1), l0, h0);
+      col_bounds(p, b, min(n0 + BN, p.Skv) - 1, l1, h1);
+      q_lo = max(q_lo, l0);
+      q_hi = min(q_hi, h1);
+    }
     col_bounds(p, b, min(nw, p.Skv - 1), l0, h0);
     col_bounds(p, b, nlast, l1, h1);
     w_lo = max(w_lo, l0);
@@ -603,6 +605,10 @@ void bwd_dkdv_f32_kernel(BwdArgs a) {
   for (int db = 0; db < C::DB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
+
+  // Staged dS: this wave's 128-row KV block and its 32-row slice of it.
+  const int nkb = (p.Skv + kDsKB - 1) / kDsKB;
+  const int kb_w = nw / kDsKB, c_w = (nw % kDsKB) / kTile;
 
   const int m_first = (q_lo / kTile) * kTile;
   const int nq = q_hi > m_first ? (q_hi - m_first + kTile - 1) / kTile : 0;  // query tiles per head
@@ -693,6 +699,19 @@ void bwd_dkdv_f32_kernel(BwdArgs a) {
       // dV^T += dO^T P and dK^T += Q^T dS: A = dO / Q[row of step r][32 db + l32]
       rsum2<C::DB, C::P>(sO[buf], s, dv, sQ[buf], dp, dk, l32, h);
     }
+    if constexpr (DS) {
+      // this wave's 32 x 32 slice of the (query tile, KV block) unit: dS as
+      // fed to dK (zero where skipped or masked), rows = query rows
+      const int t = m0 / kDsQT;
+      const int kb_lo = ds_kb_lo(t, p.window, nkb);
+      if (kb_w < nkb && kb_w >= kb_lo && kb_w < ds_kb_hi(t, p.causal, nkb)) {
+        const int64_t unit = (int64_t)(b * p.Hq + hq) * a.ds_head + ds_tile_offset(t, p.causal, p.window, nkb) +
+                             (kb_w - kb_lo);
+        float* dst = (float*)(a.ds + unit * kDsUnitB32) + c_w * (kTile * kTile) + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) __builtin_nontemporal_store(dp[r], dst + blk_row(r, h) * kTile);
+      }
+    }
     if (more) {
       st.store(sO[buf ^ 1], tid);
       store_rows(buf ^ 1);
@@ -718,6 +737,106 @@ void bwd_dkdv_f32_kernel(BwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// dQ = dS K from the fp32 dS the dK/dV kernel staged (no S or dP recompute):
+// each wave owns 32 query rows (one dS unit row band) and streams 32-row K
+// tiles over the band of KV blocks of its query tile.
+template <int D>
+struct F32DqDs {
+  static constexpr int NW = 8;
+  static constexpr int WPE = 2;
+  static constexpr int BM = 32 * NW;
+};
+
+template <int D>
+__global__ __launch_bounds__(F32DqDs<D>::NW * 64) __attribute__((amdgpu_waves_per_eu(F32DqDs<D>::WPE, F32DqDs<D>::WPE)))
+void bwd_dq_ds_f32_kernel(BwdArgs a) {
+  using namespace f32m;
+  constexpr int NW = F32DqDs<D>::NW, BM = F32DqDs<D>::BM;
+  using C = Cfg<D, NW>;
+  __shared__ __attribute__((aligned(16))) float sK[2][C::TILE];
+  const Shape& p = a.p;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, h = lane >> 5;
+  const int nbh = p.B * p.Hq;
+  int kq, bh;
+  if (!xcd_lpt_item(blockIdx.x, a.ntiles, nbh, kq, bh)) {
+    kq = blockIdx.x / nbh;
+    bh = blockIdx.x % nbh;
+  }
+  const int qt = a.ntiles - 1 - kq;
+  const int hq = bh % p.Hq, b = bh / p.Hq, hk = hq / p.G;
+  const int m0 = qt * BM, mw = m0 + 32 * wave, my_m = mw + l32;
+  const float* kp = (const float*)a.k.data + b * a.k.sb + hk * a.k.sh;
+  const int nkb = (p.Skv + kDsKB - 1) / kDsKB;
+
+  // KV blocks of this wave's query tile, and of the workgroup's tiles
+  const bool wave_live = mw < p.Sq;
+  const int t = mw / kDsQT;
+  const int w_kb_lo = ds_kb_lo(t, p.window, nkb), w_kb_hi = wave_live ? ds_kb_hi(t, p.causal, nkb) : 0;
+  const int t_first = m0 / kDsQT, t_last = (min(m0 + BM, p.Sq) - 1) / kDsQT;
+  const int kv_lo = kDsKB * ds_kb_lo(t_first, p.window, nkb);
+  const int kv_hi = min(p.Skv, kDsKB * ds_kb_hi(t_last, p.causal, nkb));
+  // unit of block kb for this wave: ubase + kb
+  const int64_t ubase = (int64_t)(b * p.Hq + hq) * a.ds_head + ds_tile_offset(t, p.causal, p.window, nkb) - w_kb_lo;
+  const float* dsb = (const float*)a.ds + l32 * kTile + 4 * h;
+
+  f32x16 acc[C::DB];
+#pragma unroll
+  for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+
+  // dS^T operand of one 32-row K tile: element r = dS[my_m][n0 + row of step r]
+  auto load_ds = [&](int n0, f32x16& x) {
+    const int kb = n0 / kDsKB;
+    if (kb >= w_kb_lo && kb < w_kb_hi) {
+      const float* src = dsb + (ubase + kb) * (kDsUnitB32 / 4) + ((n0 % kDsKB) / kTile) * (kTile * kTile);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 v = *(const f32x4*)(src + 8 * j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[4 * j + e] = v[e];
+      }
+    }
+  };
+
+  Tile<D, NW> st;
+  f32x16 cur, nxt;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) cur[r] = nxt[r] = 0.f;
+  if (kv_lo < kv_hi) {
+    st.load(kp, a.k.ss, kv_lo, p.Skv, tid);
+    load_ds(kv_lo, cur);
+    st.store(sK[0], tid);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int n0 = kv_lo; n0 < kv_hi; n0 += kTile, buf ^= 1) {
+    const bool more = n0 + kTile < kv_hi;
+    if (more) {
+      st.load(kp, a.k.ss, n0 + kTile, p.Skv, tid);
+      load_ds(n0 + kTile, nxt);
+    }
+    const int kb = n0 / kDsKB;
+    if (kb >= w_kb_lo && kb < w_kb_hi) rsum<C::DB, C::P>(sK[buf], l32, h, cur, acc);
+    if (more) st.store(sK[buf ^ 1], tid);
+    __syncthreads();
+    cur = nxt;
+  }
+  if (my_m < p.Sq) {
+    float* op = (float*)a.dq.data + b * a.dq.sb + hq * a.dq.sh + (int64_t)my_m * a.dq.ss;
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[db][4 * i + e];
+        *(f32x4*)(op + 32 * db + 8 * i + 4 * h) = v;
+      }
+  }
+}
+
 // The four (soft-cap, ALiBi) instances of a kernel.
 #define FLEXATT_F32_LAUNCH(kern, grid, block, st, x)                                           \
   do {                                                                                          \
@@ -726,6 +845,16 @@ void bwd_dkdv_f32_kernel(BwdArgs a) {
     else if (sc_) hipLaunchKernelGGL((kern<FLEXATT_D, true, false>), grid, block, 0, st, x);    \
     else if (al_) hipLaunchKernelGGL((kern<FLEXATT_D, false, true>), grid, block, 0, st, x);    \
     else hipLaunchKernelGGL((kern<FLEXATT_D, false, false>), grid, block, 0, st, x);            \
+  } while (0)
+
+// The same with a fourth template argument.
+#define FLEXATT_F32_LAUNCH4(kern, X, grid, block, st, x)                                            \
+  do {                                                                                              \
+    const bool sc_ = (x).p.cap > 0.f, al_ = (x).p.alibi != nullptr;                                 \
+    if (sc_ && al_) hipLaunchKernelGGL((kern<FLEXATT_D, true, true, X>), grid, block, 0, st, x);    \
+    else if (sc_) hipLaunchKernelGGL((kern<FLEXATT_D, true, false, X>), grid, block, 0, st, x);     \
+    else if (al_) hipLaunchKernelGGL((kern<FLEXATT_D, false, true, X>), grid, block, 0, st, x);     \
+    else hipLaunchKernelGGL((kern<FLEXATT_D, false, false, X>), grid, block, 0, st, x);             \
   } while (0)
 
 #define FLEXATT_CAT2(a, b) a##b
@@ -751,7 +880,21 @@ hipError_t FLEXATT_CAT(bwd_dkdv_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t 
   using F = F32Kv<FLEXATT_D>;
   BwdArgs x = a;
   x.ntiles = (a.p.Skv + F::BN - 1) / F::BN;
-  FLEXATT_F32_LAUNCH(bwd_dkdv_f32_kernel, dim3(x.ntiles * a.p.B * a.p.Hkv), dim3(F::NW * 64), st, x);
+  FLEXATT_F32_LAUNCH4(bwd_dkdv_f32_kernel, false, dim3(x.ntiles * a.p.B * a.p.Hkv), dim3(F::NW * 64), st, x);
+  return hipGetLastError();
+}
+hipError_t FLEXATT_CAT(bwd_kv_ds_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
+  using F = F32Kv<FLEXATT_D>;
+  BwdArgs x = a;
+  x.ntiles = (a.p.Skv + F::BN - 1) / F::BN;
+  FLEXATT_F32_LAUNCH4(bwd_dkdv_f32_kernel, true, dim3(x.ntiles * a.p.B * a.p.Hkv), dim3(F::NW * 64), st, x);
+  return hipGetLastError();
+}
+hipError_t FLEXATT_CAT(bwd_dq_ds_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
+  using F = F32DqDs<FLEXATT_D>;
+  BwdArgs x = a;
+  x.ntiles = (a.p.Sq + F::BM - 1) / F::BM;
+  hipLaunchKernelGGL((bwd_dq_ds_f32_kernel<FLEXATT_D>), dim3(x.ntiles * a.p.B * a.p.Hq), dim3(F::NW * 64), 0, st, x);
   return hipGetLastError();
 }
 #endif

@@ -412,6 +412,11 @@ __device__ __forceinline__ bool block_on(const Shape& p, int b, int hq, int i, i
 constexpr int kDsQT = 32;     // query rows per dS unit
 constexpr int kDsKB = 128;    // KV rows per dS unit
 constexpr int kDsUnitB = 8192;  // bytes per dS unit (16-bit elements)
+// fp32 inputs stage dS in fp32 over the same units (32 query rows x 128 KV
+// rows, same band and offsets), laid out as 4 slices of 32 KV rows, each
+// [query row][KV row] row-major: element (i, j) of the unit at
+// ((j / 32) * 32 + i) * 32 + j % 32.
+constexpr int kDsUnitB32 = 16384;
 
 __host__ __device__ __forceinline__ int ds_kb_lo(int t, int window, int nkb) {
   if (window <= 0) return 0;

@@ -121,6 +121,13 @@ hipError_t bwd_dkdv_f32_d32(const BwdArgs&, hipStream_t);
 hipError_t bwd_dkdv_f32_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_dkdv_f32_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_simt_f32_d256(const BwdArgs&, hipStream_t);
+// fp32 dK/dV writing its dS in fp32, and dQ = dS K from it (D <= 128).
+hipError_t bwd_kv_ds_f32_d32(const BwdArgs&, hipStream_t);
+hipError_t bwd_kv_ds_f32_d64(const BwdArgs&, hipStream_t);
+hipError_t bwd_kv_ds_f32_d128(const BwdArgs&, hipStream_t);
+hipError_t bwd_dq_ds_f32_d32(const BwdArgs&, hipStream_t);
+hipError_t bwd_dq_ds_f32_d64(const BwdArgs&, hipStream_t);
+hipError_t bwd_dq_ds_f32_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_dkdv_simt_f32_d256(const BwdArgs&, hipStream_t);
 
 // dQ as a query-stationary tile stream (bwd_q.hip), D = 128; with

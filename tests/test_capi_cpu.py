@@ -280,7 +280,11 @@ def test_bwd_workspace_range():
     assert ws(problem(head_dim=64)) == ws(problem(head_dim=128))  # 2 bytes per pair whatever D
     assert ws(problem(head_dim=256)) == ws(problem(head_dim=128))
     assert ws(problem(head_dim=32)) == 0
-    assert ws(problem(head_dim=128, dtype=L.F32)) == 0
+    # fp32 stages dS in fp32 over the same units: 4 bytes per pair, D <= 128
+    band = ws(problem(head_dim=128)) - L.BWD_QUEUE_BYTES
+    for d in (32, 64, 128):
+        assert ws(problem(head_dim=d, dtype=L.F32)) == 2 * band + L.BWD_QUEUE_BYTES
+    assert ws(problem(head_dim=256, dtype=L.F32)) == 0
     # masks keep the causal / window band of stored units (masked entries hold zeros)
     assert ws(problem(head_dim=128, doc_bounds=FAKE)) == ws(problem(head_dim=128))
     assert ws(problem(head_dim=128, block_map=FAKE, block_heads=1)) == ws(problem(head_dim=128))
