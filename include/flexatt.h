@@ -180,7 +180,7 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
 #define FLEXATT_BWD_QUEUE_BYTES 256
 
 /* Backward with dS staged through HBM (fp16/bf16 at head_dim 64, 128 or
- * 256; fp32 at head_dim 32, 64 or 128).  The dK/dV kernel already forms dS
+ * 256; fp32 at every head_dim).  The dK/dV kernel already forms dS
  * for every attended pair; it writes those values (rounded to the input
  * dtype, as its own dK MFMAs consume them) to a caller-owned workspace, and
  * the dQ kernel forms dQ = scale * dS K from them instead of recomputing S

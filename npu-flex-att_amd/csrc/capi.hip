@@ -126,8 +126,8 @@ Shape make_shape(const flexatt_problem* p) {
 View view(const flexatt_tensor* t) { return View{t->data, t->stride_b, t->stride_h, t->stride_s}; }
 MutView mview(const flexatt_tensor* t) { return MutView{t->data, t->stride_b, t->stride_h, t->stride_s}; }
 
-// [dtype][head index]; fp32 on the fp32 matrix cores except the D = 256
-// backward (vector ALU kernels)
+// [dtype][head index]; fp32 on the fp32 matrix cores except the recomputing
+// dQ at D = 256 (vector ALU kernel)
 const FwdLauncher kFwd[3][4] = {
     {fwd_f32_d32, fwd_f32_d64, fwd_f32_d128, fwd_f32_d256},
     {fwd_mfma_f16_d32, fwd_mfma_f16_d64, fwd_mfma_f16_d128, fwd_mfma_f16_d256},
@@ -139,7 +139,7 @@ const BwdLauncher kDq[3][4] = {
     {bwd_dq_mfma_bf16_d32, bwd_dq_mfma_bf16_d64, bwd_q_bf16_d128, bwd_dq_mfma_bf16_d256},
 };
 const BwdLauncher kDkdv[3][4] = {
-    {bwd_dkdv_f32_d32, bwd_dkdv_f32_d64, bwd_dkdv_f32_d128, bwd_dkdv_simt_f32_d256},
+    {bwd_dkdv_f32_d32, bwd_dkdv_f32_d64, bwd_dkdv_f32_d128, bwd_dkdv_f32_d256},
     {bwd_dkdv_mfma_f16_d32, bwd_kv_f16_d64, bwd_kv_f16_d128, bwd_kv_f16_d256},
     {bwd_dkdv_mfma_bf16_d32, bwd_kv_bf16_d64, bwd_kv_bf16_d128, bwd_kv_bf16_d256},
 };
@@ -294,19 +294,21 @@ int bwd_common(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_
   return FLEXATT_OK;
 }
 
-// Staged dS (fp16/bf16 at D = 64, 128 and 256; fp32 at D = 32, 64 and 128;
+// Staged dS (fp16/bf16 at D = 64, 128 and 256; fp32 at every D;
 // every mask primitive: the dK/dV kernel masks per element and stores every
 // unit of the causal / window band, zero where masked): units per query head
 // and workspace bytes; 0 when the problem takes the recomputing dQ kernel.
 bool ds_applies(const flexatt_problem* p) {
-  if (p->dtype == FLEXATT_F32) return p->head_dim <= 128;
+  if (p->dtype == FLEXATT_F32) return true;
   return (p->dtype == FLEXATT_F16 || p->dtype == FLEXATT_BF16) &&
          (p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256);
 }
 int64_t ds_unit_bytes(const flexatt_problem* p) { return p->dtype == FLEXATT_F32 ? kDsUnitB32 : kDsUnitB; }
 BwdLauncher pick_kv_ds(const flexatt_problem* p) {
   if (p->dtype == FLEXATT_F32)
-    return p->head_dim == 32 ? bwd_kv_ds_f32_d32 : (p->head_dim == 64 ? bwd_kv_ds_f32_d64 : bwd_kv_ds_f32_d128);
+    return p->head_dim == 32 ? bwd_kv_ds_f32_d32
+           : p->head_dim == 64 ? bwd_kv_ds_f32_d64
+           : p->head_dim == 128 ? bwd_kv_ds_f32_d128 : bwd_kv_ds_f32_d256;
   const bool bf = p->dtype == FLEXATT_BF16;
   if (p->head_dim == 64) return bf ? bwd_kv_ds_bf16_d64 : bwd_kv_ds_f16_d64;
   if (p->head_dim == 256) return bf ? bwd_kv_ds_bf16_d256 : bwd_kv_ds_f16_d256;
@@ -314,7 +316,9 @@ BwdLauncher pick_kv_ds(const flexatt_problem* p) {
 }
 BwdLauncher pick_dq_ds(const flexatt_problem* p) {
   if (p->dtype == FLEXATT_F32)
-    return p->head_dim == 32 ? bwd_dq_ds_f32_d32 : (p->head_dim == 64 ? bwd_dq_ds_f32_d64 : bwd_dq_ds_f32_d128);
+    return p->head_dim == 32 ? bwd_dq_ds_f32_d32
+           : p->head_dim == 64 ? bwd_dq_ds_f32_d64
+           : p->head_dim == 128 ? bwd_dq_ds_f32_d128 : bwd_dq_ds_f32_d256;
   const bool bf = p->dtype == FLEXATT_BF16;
   if (p->head_dim == 64) return bf ? bwd_dq_ds_bf16_d64 : bwd_dq_ds_f16_d64;
   if (p->head_dim == 256) return bf ? bwd_dq_ds_bf16_d256 : bwd_dq_ds_f16_d256;

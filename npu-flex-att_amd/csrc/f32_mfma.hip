@@ -18,14 +18,15 @@
 //   C/D        acc[4*i + j] = C[row = 8*i + 4*(l/32) + j][col = l%32]
 // A product over the head dim runs as D/2 MFMAs; wave half h takes
 // d = h*D/2 + s at step s, so that each lane reads its operand rows as
-// contiguous 16-byte groups.  A product over 32 rows (P V, dS K, P^T dO,
-// dS^T Q) takes at step r the rows 8*(r/4) + 4h + r%4 -- exactly the rows
+// contiguous 16-byte groups.  A product over 32 rows (P V, dS K) takes at
+// step r the rows 8*(r/4) + 4h + r%4 -- exactly the rows
 // whose scores lane half h holds in accumulator element r, so the scores
 // feed the B operand from their own registers.
 //
 // Forward and dQ keep the query rows as the accumulator columns
 // (S^T = K Q^T, one query row per lane); dK/dV keeps the KV rows as columns
-// (S = Q K^T, one KV row per lane).  K/V (or Q/dO) tiles of 32 rows pass
+// (S = Q K^T, one KV row per lane, on the 16 x 16 x 4 MFMA, whose layout is
+// given with it below).  K/V (or Q/dO) tiles of 32 rows pass
 // through registers into a double-buffered LDS tile with rows padded to
 // D + 4 floats (16-byte row reads and 4-byte column reads both without bank
 // conflicts), one barrier per tile.
@@ -155,37 +156,74 @@ __device__ __forceinline__ void rsum(const float* t, int l32, int h, const f32x1
     __builtin_amdgcn_sched_barrier(0);
   }
 }
-// Two such sums with the same rows of two tiles.
-template <int DB, int P>
-__device__ __forceinline__ void rsum2(const float* t1, const f32x16& x1, f32x16 (&acc1)[DB], const float* t2,
-                                      const f32x16& x2, f32x16 (&acc2)[DB], int l32, int h) {
+// --- 16 x 16 x 4 fp32 MFMA (16 accumulator columns per wave) -----------------
+//   A operand  lane l holds A[row = l%16][k = l/16]
+//   B operand  lane l holds B[k = l/16][col = l%16]
+//   C/D        acc[r] = C[row = 4*(l/16) + r][col = l%16]
+// Head-dim sums: lane group g = l/16 takes d = g*D/4 + s at step s.  16-row
+// sums: at step s group g takes row 4g + s, the row of its accumulator
+// element s.
+__device__ __forceinline__ f32x4 mma16(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+// acc1 += A1 B1^T and acc2 += A2 B2^T over the head dim (A rows from LDS,
+// 16-byte reads one group of four MFMAs ahead; B from registers).
+template <int HD4>
+__device__ __forceinline__ void dsum16x2(const float* t1, const float (&b1)[HD4], f32x4& acc1, const float* t2,
+                                         const float (&b2)[HD4], f32x4& acc2) {
+  f32x4 c1 = lds4(t1), c2 = lds4(t2);
+#pragma unroll
+  for (int k4 = 0; k4 < HD4; k4 += 4) {
+    f32x4 n1 = c1, n2 = c2;
+    if (k4 + 4 < HD4) {
+      n1 = lds4(t1 + k4 + 4);
+      n2 = lds4(t2 + k4 + 4);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc1 = mma16(c1[e], b1[k4 + e], acc1);
+      acc2 = mma16(c2[e], b2[k4 + e], acc2);
+    }
+    c1 = n1;
+    c2 = n2;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+// acc1[db] += A1^T x1 and acc2[db] += A2^T x2 over the 32 rows of a tile
+// (two 16-row blocks qb): A column 16 db + l16 of t1 / t2 at row
+// 16 qb + 4 g + s, x = the lane's element s of block qb.
+template <int DB16, int P>
+__device__ __forceinline__ void rsum16x2(const float* t1, const f32x4 (&x1)[2], f32x4 (&acc1)[DB16],
+                                         const float* t2, const f32x4 (&x2)[2], f32x4 (&acc2)[DB16], int l16,
+                                         int g) {
+  constexpr int NG = 2 * DB16;  // groups of four MFMA steps: (db, qb)
   float c1[4], c2[4], n1[4], n2[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    c1[i] = t1[blk_row(i, h) * P + l32];
-    c2[i] = t2[blk_row(i, h) * P + l32];
+    c1[i] = t1[(4 * g + i) * P + l16];
+    c2[i] = t2[(4 * g + i) * P + l16];
   }
 #pragma unroll
-  for (int g = 0; g < 4 * DB; ++g) {
-    const int db = g >> 2, r0 = 4 * (g & 3);
+  for (int q = 0; q < NG; ++q) {
+    const int db = q >> 1, qb = q & 1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       n1[i] = c1[i];
       n2[i] = c2[i];
     }
-    if (g + 1 < 4 * DB) {
-      const int db1 = (g + 1) >> 2, r1 = 4 * ((g + 1) & 3);
+    if (q + 1 < NG) {
+      const int db1 = (q + 1) >> 1, qb1 = (q + 1) & 1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int off = blk_row(r1 + i, h) * P + 32 * db1 + l32;
+        const int off = (16 * qb1 + 4 * g + i) * P + 16 * db1 + l16;
         n1[i] = t1[off];
         n2[i] = t2[off];
       }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      acc1[db] = mma(c1[i], x1[r0 + i], acc1[db]);
-      acc2[db] = mma(c2[i], x2[r0 + i], acc2[db]);
+      acc1[db] = mma16(c1[i], x1[qb][i], acc1[db]);
+      acc2[db] = mma16(c2[i], x2[qb][i], acc2[db]);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -519,28 +557,36 @@ void bwd_dq_f32_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV: each wave owns 32 KV rows (the accumulator columns) and streams
-// 32-row Q/dO tiles of every query head of its group: S = Q K^T,
-// dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS.
+// dK/dV: each wave owns 16 KV rows (the accumulator columns of the
+// 16 x 16 x 4 MFMA) and streams 32-row Q/dO tiles of every query head of
+// its group: S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS.  K, V,
+// dK and dV take D/4 values per lane, so two waves share a SIMD at
+// D <= 128 and D = 256 fits one wave's registers (32 KV rows per wave on the
+// 32 x 32 x 2 MFMA need D/2 each: one wave per SIMD at D = 128, 1.3x
+// slower).  With DS the kernel also stores the dS it feeds dK into the
+// staged-dS units: every (query tile, 128-row block) unit of the causal /
+// window band that its rows fall in, zeros where a wave skips or masks.
 template <int D>
-struct F32Kv {
-  static constexpr int NW = D == 128 ? 4 : 8;
-  static constexpr int WPE = D == 128 ? 1 : 2;
-  static constexpr int BN = 32 * NW;  // KV rows per workgroup
+struct F32Kv16 {
+  static constexpr int NW = D == 256 ? 4 : 8;
+  static constexpr int WPE = D == 256 ? 1 : 2;
+  static constexpr int BN = 16 * NW;  // KV rows per workgroup
 };
 
 template <int D, bool SOFTCAP, bool ALIBI, bool DS>
-__global__ __launch_bounds__(F32Kv<D>::NW * 64) __attribute__((amdgpu_waves_per_eu(F32Kv<D>::WPE, F32Kv<D>::WPE)))
-void bwd_dkdv_f32_kernel(BwdArgs a) {
+__global__ __launch_bounds__(F32Kv16<D>::NW * 64)
+__attribute__((amdgpu_waves_per_eu(F32Kv16<D>::WPE, F32Kv16<D>::WPE)))
+void bwd_dkdv16_f32_kernel(BwdArgs a) {
   using namespace f32m;
-  constexpr int NW = F32Kv<D>::NW, BN = F32Kv<D>::BN;
+  constexpr int NW = F32Kv16<D>::NW, BN = F32Kv16<D>::BN;
+  constexpr int HD4 = D / 4, DB16 = D / 16;
   using C = Cfg<D, NW>;
   __shared__ __attribute__((aligned(16))) float sQ[2][C::TILE];
   __shared__ __attribute__((aligned(16))) float sO[2][C::TILE];
   __shared__ __attribute__((aligned(16))) float sL[2][kTile];
   __shared__ __attribute__((aligned(16))) float sDl[2][kTile];
   const Shape& p = a.p;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, h = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g = lane >> 4;
   const int nbh = p.B * p.Hkv;
   int kt, bh;
   if (!xcd_lpt_item(blockIdx.x, a.ntiles, nbh, kt, bh)) {  // causal: low KV tiles are the longest
@@ -548,18 +594,18 @@ void bwd_dkdv_f32_kernel(BwdArgs a) {
     bh = blockIdx.x % nbh;
   }
   const int hk = bh % p.Hkv, b = bh / p.Hkv;
-  const int n0 = kt * BN, nw = n0 + 32 * wave, my_n = nw + l32;
+  const int n0 = kt * BN, nw = n0 + 16 * wave, my_n = nw + l16;
   const float* kp = (const float*)a.k.data + b * a.k.sb + hk * a.k.sh;
   const float* vp = (const float*)a.v.data + b * a.v.sb + hk * a.v.sh;
 
-  // K and V as the B operands of S = Q K^T and dP = dO V^T.
-  float kr[C::HD], vr[C::HD];
+  // K and V as the B operands of S = Q K^T and dP = dO V^T: K[my_n][g*D/4 + s].
+  float kr[HD4], vr[HD4];
   {
     const int rn = min(my_n, p.Skv - 1);
-    const float* s1 = kp + (int64_t)rn * a.k.ss + h * C::HD;
-    const float* s2 = vp + (int64_t)rn * a.v.ss + h * C::HD;
+    const float* s1 = kp + (int64_t)rn * a.k.ss + g * HD4;
+    const float* s2 = vp + (int64_t)rn * a.v.ss + g * HD4;
 #pragma unroll
-    for (int s = 0; s < C::HD; s += 4) {
+    for (int s = 0; s < HD4; s += 4) {
       const f32x4 x = *(const f32x4*)(s1 + s);
       const f32x4 y = *(const f32x4*)(s2 + s);
 #pragma unroll
@@ -573,7 +619,11 @@ void bwd_dkdv_f32_kernel(BwdArgs a) {
   // Query range of the workgroup, of this wave, and the query interval of this KV row.
   int q_lo = p.causal ? n0 : 0, q_hi = p.Sq;
   if (p.window > 0) q_hi = min(q_hi, n0 + BN + p.window);
-  const int nlast = min(nw + 31, p.Skv - 1);
+  if constexpr (DS) {  // the whole band of the 128-row dS blocks the workgroup's rows fall in
+    if (p.causal) q_lo = kDsKB * (n0 / kDsKB);
+    if (p.window > 0) q_hi = min(p.Sq, kDsKB * ((n0 + BN - 1) / kDsKB + 1) + p.window);
+  }
+  const int nlast = min(nw + 15, p.Skv - 1);
   const bool wave_live = nw < p.Skv;
   int w_lo = q_lo, w_hi = q_hi;
   if (p.causal) w_lo = max(w_lo, nw);
@@ -600,26 +650,25 @@ void bwd_dkdv_f32_kernel(BwdArgs a) {
   if (my_n >= p.Skv) col_hi = col_lo;
   const unsigned col_w = (unsigned)max(col_hi - col_lo, 0);
 
-  f32x16 dk[C::DB], dv[C::DB];
+  f32x4 dk[DB16], dv[DB16];
 #pragma unroll
-  for (int db = 0; db < C::DB; ++db)
+  for (int db = 0; db < DB16; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
+    for (int r = 0; r < 4; ++r) dk[db][r] = dv[db][r] = 0.f;
 
-  // Staged dS: this wave's 128-row KV block and its 32-row slice of it.
+  // Staged dS: this wave's 128-row KV block and its column offset in the block.
   const int nkb = (p.Skv + kDsKB - 1) / kDsKB;
-  const int kb_w = nw / kDsKB, c_w = (nw % kDsKB) / kTile;
+  const int kb_w = nw / kDsKB, j_w = nw % kDsKB + l16;
 
   const int m_first = (q_lo / kTile) * kTile;
   const int nq = q_hi > m_first ? (q_hi - m_first + kTile - 1) / kTile : 0;  // query tiles per head
   const int total = nq * p.G;
   Tile<D, NW> st;
   float lv = 0.f, dv0 = 0.f;  // LSE and Delta of one query row (threads < 32)
-  // step u: query head g = u / nq, tile m0 = m_first + kTile * (u % nq)
   auto step_ptrs = [&](int u, const float*& qp, const float*& dop, int& m, int& hq) {
-    const int g = u / nq;
+    const int gg = u / nq;
     m = m_first + kTile * (u % nq);
-    hq = hk * p.G + g;
+    hq = hk * p.G + gg;
     qp = (const float*)a.q.data + b * a.q.sb + hq * a.q.sh;
     dop = (const float*)a.dout.data + b * a.dout.sb + hq * a.dout.sh;
   };
@@ -663,53 +712,60 @@ void bwd_dkdv_f32_kernel(BwdArgs a) {
       st.load(nqp, a.q.ss, nm, p.Sq, tid);
       load_rows(nm, nhq);
     }
-    const int g = u / nq, m0 = m_first + kTile * (u % nq);
-    const int hq = hk * p.G + g;
+    const int m0 = m_first + kTile * (u % nq);
+    const int hq = hk * p.G + u / nq;
     const bool on = wave_live && m0 < w_hi && m0 + kTile > w_lo &&
                     (!p.blk || block_row(p, b, hq, m0)[nw / kBlk] != 0);
-    f32x16 s, dp;
+    f32x4 s[2], dp[2];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
-    const int ro = l32 * C::P + h * C::HD;
-    if (on) dsum2<C::HD, C::P>(sQ[buf] + ro, kr, s, sO[buf] + ro, vr, dp);
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[qb][r] = dp[qb][r] = 0.f;
+    if (on) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const int ro = (16 * qb + l16) * C::P + g * HD4;
+        dsum16x2<HD4>(sQ[buf] + ro, kr, s[qb], sO[buf] + ro, vr, dp[qb]);
+      }
+    }
     if (more) {
       st.store(sQ[buf ^ 1], tid);
       st.load(ndop, a.dout.ss, nm, p.Sq, tid);
     }
     if (on) {
       const float slope = ALIBI ? p.alibi[hq] : 0.f;
-      const int a0 = col_lo - m0 - 4 * h;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x4 l4 = lds4(&sL[buf][8 * i + 4 * h]);
-        const f32x4 d4 = lds4(&sDl[buf][8 * i + 4 * h]);
+      for (int qb = 0; qb < 2; ++qb) {
+        const f32x4 l4 = lds4(&sL[buf][16 * qb + 4 * g]);
+        const f32x4 d4 = lds4(&sDl[buf][16 * qb + 4 * g]);
+        const int a0 = col_lo - m0 - 16 * qb - 4 * g;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * i + e;
-          const int mi = m0 + blk_row(r, h);
+        for (int r = 0; r < 4; ++r) {
+          const int mi = m0 + 16 * qb + 4 * g + r;
           float t = 0.f;
-          const float x = score<SOFTCAP, ALIBI>(s[r], p, slope, mi, my_n, t);
-          const float pj = (unsigned)(8 * i + e - a0) < col_w ? expf(x - l4[e]) : 0.f;
-          float d = pj * (dp[r] - d4[e]) * p.scale;
+          const float x = score<SOFTCAP, ALIBI>(s[qb][r], p, slope, mi, my_n, t);
+          const float pj = (unsigned)(r - a0) < col_w ? expf(x - l4[r]) : 0.f;
+          float d = pj * (dp[qb][r] - d4[r]) * p.scale;
           if constexpr (SOFTCAP) d *= (1.0f - t * t);
-          s[r] = pj;
-          dp[r] = d;
+          s[qb][r] = pj;
+          dp[qb][r] = d;
         }
       }
-      // dV^T += dO^T P and dK^T += Q^T dS: A = dO / Q[row of step r][32 db + l32]
-      rsum2<C::DB, C::P>(sO[buf], s, dv, sQ[buf], dp, dk, l32, h);
+      // dV^T += dO^T P and dK^T += Q^T dS over the tile's 32 query rows
+      rsum16x2<DB16, C::P>(sO[buf], s, dv, sQ[buf], dp, dk, l16, g);
     }
     if constexpr (DS) {
-      // this wave's 32 x 32 slice of the (query tile, KV block) unit: dS as
-      // fed to dK (zero where skipped or masked), rows = query rows
       const int t = m0 / kDsQT;
       const int kb_lo = ds_kb_lo(t, p.window, nkb);
       if (kb_w < nkb && kb_w >= kb_lo && kb_w < ds_kb_hi(t, p.causal, nkb)) {
         const int64_t unit = (int64_t)(b * p.Hq + hq) * a.ds_head + ds_tile_offset(t, p.causal, p.window, nkb) +
                              (kb_w - kb_lo);
-        float* dst = (float*)(a.ds + unit * kDsUnitB32) + c_w * (kTile * kTile) + l32;
+        // element (query row i, KV column j) of the unit at ((j / 32) * 32 + i) * 32 + j % 32
+        float* dst = (float*)(a.ds + unit * kDsUnitB32) + (j_w / kTile) * (kTile * kTile) + j_w % kTile;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) __builtin_nontemporal_store(dp[r], dst + blk_row(r, h) * kTile);
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) __builtin_nontemporal_store(dp[qb][r], dst + (16 * qb + 4 * g + r) * kTile);
       }
     }
     if (more) {
@@ -722,18 +778,10 @@ void bwd_dkdv_f32_kernel(BwdArgs a) {
     float* kd = (float*)a.dk.data + b * a.dk.sb + hk * a.dk.sh + (int64_t)my_n * a.dk.ss;
     float* vd = (float*)a.dv.data + b * a.dv.sb + hk * a.dv.sh + (int64_t)my_n * a.dv.ss;
 #pragma unroll
-    for (int db = 0; db < C::DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f32x4 x, y;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          x[e] = dk[db][4 * i + e];
-          y[e] = dv[db][4 * i + e];
-        }
-        *(f32x4*)(kd + 32 * db + 8 * i + 4 * h) = x;
-        *(f32x4*)(vd + 32 * db + 8 * i + 4 * h) = y;
-      }
+    for (int db = 0; db < DB16; ++db) {
+      *(f32x4*)(kd + 16 * db + 4 * g) = dk[db];
+      *(f32x4*)(vd + 16 * db + 4 * g) = dv[db];
+    }
   }
 }
 
@@ -876,18 +924,19 @@ hipError_t FLEXATT_CAT(bwd_dq_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st
   FLEXATT_F32_LAUNCH(bwd_dq_f32_kernel, dim3(x.ntiles * a.p.B * a.p.Hq), dim3(F::NW * 64), st, x);
   return hipGetLastError();
 }
+#endif
 hipError_t FLEXATT_CAT(bwd_dkdv_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
-  using F = F32Kv<FLEXATT_D>;
+  using F = F32Kv16<FLEXATT_D>;
   BwdArgs x = a;
   x.ntiles = (a.p.Skv + F::BN - 1) / F::BN;
-  FLEXATT_F32_LAUNCH4(bwd_dkdv_f32_kernel, false, dim3(x.ntiles * a.p.B * a.p.Hkv), dim3(F::NW * 64), st, x);
+  FLEXATT_F32_LAUNCH4(bwd_dkdv16_f32_kernel, false, dim3(x.ntiles * a.p.B * a.p.Hkv), dim3(F::NW * 64), st, x);
   return hipGetLastError();
 }
 hipError_t FLEXATT_CAT(bwd_kv_ds_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
-  using F = F32Kv<FLEXATT_D>;
+  using F = F32Kv16<FLEXATT_D>;
   BwdArgs x = a;
   x.ntiles = (a.p.Skv + F::BN - 1) / F::BN;
-  FLEXATT_F32_LAUNCH4(bwd_dkdv_f32_kernel, true, dim3(x.ntiles * a.p.B * a.p.Hkv), dim3(F::NW * 64), st, x);
+  FLEXATT_F32_LAUNCH4(bwd_dkdv16_f32_kernel, true, dim3(x.ntiles * a.p.B * a.p.Hkv), dim3(F::NW * 64), st, x);
   return hipGetLastError();
 }
 hipError_t FLEXATT_CAT(bwd_dq_ds_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
@@ -897,6 +946,5 @@ hipError_t FLEXATT_CAT(bwd_dq_ds_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t
   hipLaunchKernelGGL((bwd_dq_ds_f32_kernel<FLEXATT_D>), dim3(x.ntiles * a.p.B * a.p.Hq), dim3(F::NW * 64), 0, st, x);
   return hipGetLastError();
 }
-#endif
 
 }  // namespace flexatt

@@ -108,8 +108,9 @@ hipError_t bwd_kv_ds_f16_d256(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_bf16_d256(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_f16_d256(const BwdArgs&, hipStream_t);
 
-// fp32 inputs on the fp32 matrix cores (f32_mfma.hip): forward at every D,
-// dQ and dK/dV at D <= 128; the D = 256 backward on the vector ALUs (simt.hip).
+// fp32 inputs on the fp32 matrix cores (f32_mfma.hip): forward and dK/dV at
+// every D, dQ from the staged dS at every D, the recomputing dQ at D <= 128
+// (D = 256: on the vector ALUs, simt.hip).
 hipError_t fwd_f32_d32(const FwdArgs&, hipStream_t);
 hipError_t fwd_f32_d64(const FwdArgs&, hipStream_t);
 hipError_t fwd_f32_d128(const FwdArgs&, hipStream_t);
@@ -120,15 +121,17 @@ hipError_t bwd_dq_f32_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_dkdv_f32_d32(const BwdArgs&, hipStream_t);
 hipError_t bwd_dkdv_f32_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_dkdv_f32_d128(const BwdArgs&, hipStream_t);
+hipError_t bwd_dkdv_f32_d256(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_simt_f32_d256(const BwdArgs&, hipStream_t);
-// fp32 dK/dV writing its dS in fp32, and dQ = dS K from it (D <= 128).
+// fp32 dK/dV writing its dS in fp32, and dQ = dS K from it.
 hipError_t bwd_kv_ds_f32_d32(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_ds_f32_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_ds_f32_d128(const BwdArgs&, hipStream_t);
+hipError_t bwd_kv_ds_f32_d256(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_f32_d32(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_f32_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_f32_d128(const BwdArgs&, hipStream_t);
-hipError_t bwd_dkdv_simt_f32_d256(const BwdArgs&, hipStream_t);
+hipError_t bwd_dq_ds_f32_d256(const BwdArgs&, hipStream_t);
 
 // dQ as a query-stationary tile stream (bwd_q.hip), D = 128; with
 // a.delta_out set it also computes Delta (written there) from O and dO.

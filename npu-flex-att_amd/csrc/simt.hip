@@ -1,16 +1,16 @@
-// fp32 flash-attention backward (dQ, dK/dV) on the vector ALUs.
+// fp32 flash-attention dQ on the vector ALUs, recomputing S and dP.
 //
-// The library's fp32 path runs on the fp32 matrix cores (f32_mfma.hip); these
-// kernels serve the fp32 backward at head_dim 256, whose dK/dV would need K,
-// V, dK and dV of a 32-row block resident per lane (512 values) on the
-// matrix cores.  The reference accepts fp32 tensors on the same entry points
-// (test/test_supplementary.py:55-63; the fp32 suites of
+// The library's fp32 path runs on the fp32 matrix cores (f32_mfma.hip); this
+// kernel serves the one fp32 case left: the dQ of the backward without a dS
+// workspace (flexatt_bwd, flexatt_bwd_dq) at head_dim 256, whose Q, dO and dQ
+// rows (768 values per lane for a 32-row block) exceed one lane's registers
+// on the matrix cores.  The reference accepts fp32 tensors on the same entry
+// points (test/test_supplementary.py:55-63; the fp32 suites of
 // test/test_comprehensive.py) and expects fp32-exact results (tolerances down
-// to 1e-5, test/test_comprehensive.py:88): one 16-lane group per row, K/V (or
-// Q/dO) tiles staged in LDS, fp32 FMA, online softmax in the natural domain
-// with expf/logf/tanhf.  Semantics are those of the MFMA kernels
-// (npu_flash_attention.py:17-166, :298-402, :407-560), including the KV tail,
-// ALiBi in backward and the in-kernel GQA group sum.
+// to 1e-5, test/test_comprehensive.py:88): one 16-lane group per row, K/V
+// tiles staged in LDS, fp32 FMA, softmax terms in the natural domain with
+// expf/tanhf.  Semantics are those of the MFMA kernels
+// (npu_flash_attention.py:298-402), including the KV tail and ALiBi.
 #include "flexatt_device.h"
 #include "flexatt_kernels.h"
 
@@ -125,101 +125,6 @@ __global__ __launch_bounds__(256) void bwd_dq_simt_kernel(BwdArgs a) {
   }
 }
 
-template <int D>
-__global__ __launch_bounds__(256) void bwd_dkdv_simt_kernel(BwdArgs a) {
-  using namespace simt;
-  constexpr int E = D / kLanes;
-  __shared__ float sQ[kTile][D];
-  __shared__ float sO[kTile][D];
-  __shared__ float sL[kTile], sDl[kTile];
-  const Shape& p = a.p;
-  const int tid = threadIdx.x, rg = tid / kLanes, ln = tid % kLanes;
-  const int kt = blockIdx.x % a.ntiles, bh = blockIdx.x / a.ntiles;
-  const int hk = bh % p.Hkv, b = bh / p.Hkv;
-  const int n0 = kt * kRows, my_n = n0 + rg;
-  const float* kp = (const float*)a.k.data + b * a.k.sb + hk * a.k.sh;
-  const float* vp = (const float*)a.v.data + b * a.v.sb + hk * a.v.sh;
-  float k[E], v[E], dk[E], dv[E];
-  const int rn = min(my_n, p.Skv - 1);
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    k[e] = my_n < p.Skv ? kp[(int64_t)rn * a.k.ss + ln + kLanes * e] : 0.f;
-    v[e] = my_n < p.Skv ? vp[(int64_t)rn * a.v.ss + ln + kLanes * e] : 0.f;
-    dk[e] = dv[e] = 0.f;
-  }
-  int q_lo = p.causal ? n0 : 0, q_hi = p.Sq;
-  if (p.window > 0) q_hi = min(q_hi, n0 + kRows + p.window);
-  int dlo, dhi;  // interval masks: the query range of this KV row (column bounds)
-  col_bounds(p, b, rn, dlo, dhi);
-  if (p.docc) {
-    int l0, h0, l1, h1;
-    col_bounds(p, b, min(n0, p.Skv - 1), l0, h0);
-    col_bounds(p, b, min(n0 + kRows, p.Skv) - 1, l1, h1);
-    q_lo = max(q_lo, l0);
-    q_hi = min(q_hi, h1);
-  }
-  for (int g = 0; g < p.G; ++g) {
-    const int hq = hk * p.G + g;
-    const float slope = p.alibi ? p.alibi[hq] : 0.f;
-    const float* qp = (const float*)a.q.data + b * a.q.sb + hq * a.q.sh;
-    const float* dop = (const float*)a.dout.data + b * a.dout.sb + hq * a.dout.sh;
-    for (int m0 = (q_lo / kTile) * kTile; m0 < q_hi; m0 += kTile) {
-      __syncthreads();
-      for (int idx = tid; idx < kTile * D; idx += 256) {
-        const int r = idx / D, c = idx % D, m = m0 + r;
-        const int mc = min(m, p.Sq - 1);
-        sQ[r][c] = m < p.Sq ? qp[(int64_t)mc * a.q.ss + c] : 0.f;
-        sO[r][c] = m < p.Sq ? dop[(int64_t)mc * a.dout.ss + c] : 0.f;
-      }
-      if (tid < kTile) {
-        const int m = m0 + tid;
-        float l = kPosInf, d = 0.f;
-        if (m < p.Sq) {
-          const int64_t ri = (int64_t)(b * p.Hq + hq) * p.Sq + m;
-          l = a.lse[ri] == kNegInf ? kPosInf : a.lse[ri];
-          d = a.delta[ri];
-        }
-        sL[tid] = l;
-        sDl[tid] = d;
-      }
-      __syncthreads();
-#pragma unroll 4
-      for (int ii = 0; ii < kTile; ++ii) {
-        float s = 0.f, dpv = 0.f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          s = fmaf(sQ[ii][ln + kLanes * e], k[e], s);
-          dpv = fmaf(sO[ii][ln + kLanes * e], v[e], dpv);
-        }
-        s = group_sum(s);
-        dpv = group_sum(dpv);
-        const int m = m0 + ii;
-        float t = 0.f;
-        const float x = score(s, p, slope, m, my_n, t);
-        const float pj = (m < p.Sq && allowed(p, m, my_n) && m >= dlo && m < dhi && block_on(p, b, hq, m, my_n))
-                             ? expf(x - sL[ii])
-                             : 0.f;
-        float ds = pj * (dpv - sDl[ii]) * p.scale;
-        if (p.cap > 0.f) ds *= (1.0f - t * t);
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          dv[e] = fmaf(pj, sO[ii][ln + kLanes * e], dv[e]);
-          dk[e] = fmaf(ds, sQ[ii][ln + kLanes * e], dk[e]);
-        }
-      }
-    }
-  }
-  if (my_n < p.Skv) {
-    float* kd = (float*)a.dk.data + b * a.dk.sb + hk * a.dk.sh + (int64_t)my_n * a.dk.ss;
-    float* vd = (float*)a.dv.data + b * a.dv.sb + hk * a.dv.sh + (int64_t)my_n * a.dv.ss;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      kd[ln + kLanes * e] = dk[e];
-      vd[ln + kLanes * e] = dv[e];
-    }
-  }
-}
-
 #define FLEXATT_CAT2(a, b) a##b
 #define FLEXATT_CAT(a, b) FLEXATT_CAT2(a, b)
 #if FLEXATT_D == 256
@@ -227,12 +132,6 @@ hipError_t FLEXATT_CAT(bwd_dq_simt_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream
   BwdArgs x = a;
   x.ntiles = (a.p.Sq + simt::kRows - 1) / simt::kRows;
   hipLaunchKernelGGL((bwd_dq_simt_kernel<FLEXATT_D>), dim3(x.ntiles * a.p.B * a.p.Hq), dim3(256), 0, st, x);
-  return hipGetLastError();
-}
-hipError_t FLEXATT_CAT(bwd_dkdv_simt_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
-  BwdArgs x = a;
-  x.ntiles = (a.p.Skv + simt::kRows - 1) / simt::kRows;
-  hipLaunchKernelGGL((bwd_dkdv_simt_kernel<FLEXATT_D>), dim3(x.ntiles * a.p.B * a.p.Hkv), dim3(256), 0, st, x);
   return hipGetLastError();
 }
 

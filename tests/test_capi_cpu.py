@@ -259,6 +259,49 @@ def _staged_units(sq, skv, causal, window):
     return len(units)
 
 
+def _band(sq, skv, causal, window):
+    """(t, kb) units of the staged-dS band (ds_kb_lo / ds_kb_hi of flexatt_device.h)."""
+    nkb = -(-skv // 128)
+    band = set()
+    for t in range(-(-sq // 32)):
+        lo = min(nkb, max(0, (32 * t - window) // 128)) if window > 0 else 0
+        hi = min(nkb, t // 4 + 1) if causal else nkb
+        band.update((t, kb) for kb in range(lo, hi))
+    return band
+
+
+@pytest.mark.parametrize("bn,rows", [(64, 16), (128, 16), (128, 32), (256, 32)])
+@pytest.mark.parametrize("sq,skv", [(1, 1), (100, 70), (300, 129), (1000, 257), (129, 1000), (777, 900)])
+@pytest.mark.parametrize("causal,window", [(0, 0), (1, 0), (1, 1), (1, 100), (0, 33), (1, 300)])
+def test_f32_staged_slices_cover_the_band(bn, rows, sq, skv, causal, window):
+    """The fp32 dK/dV kernels (bn KV rows per workgroup, `rows` per wave)
+    store each `rows`-column slice of every band unit that the dQ kernel
+    reads, and none twice: a
+    workgroup at KV row n0 walks the query tiles of the whole band of the
+    128-row blocks its rows fall in (q_lo = 128 floor(n0 / 128) if causal,
+    q_hi = min(Sq, 128 (floor((n0 + bn - 1) / 128) + 1) + W) with a window)
+    and a wave stores where its block kb_w < nkb is in the tile's band."""
+    nkb = -(-skv // 128)
+    band = _band(sq, skv, causal, window)
+    stored = {}
+    for n0 in range(0, -(-skv // bn) * bn, bn):
+        q_lo = 128 * (n0 // 128) if causal else 0
+        q_hi = min(sq, 128 * ((n0 + bn - 1) // 128 + 1) + window) if window > 0 else sq
+        m_first = (q_lo // 32) * 32
+        for m0 in range(m_first, q_hi, 32):
+            t = m0 // 32
+            for nw in range(n0, n0 + bn, rows):
+                kb_w = nw // 128
+                if kb_w < nkb and (t, kb_w) in band:
+                    key = (t, kb_w, nw % 128)
+                    assert key not in stored, key
+                    stored[key] = True
+    # the dQ kernel reads the 32-row K tiles that start below Skv
+    read_end = -(-skv // 32) * 32
+    want = {(t, kb, c) for (t, kb) in band for c in range(0, 128, rows) if 128 * kb + c < read_end}
+    assert want <= set(stored)
+
+
 @pytest.mark.parametrize("sq,skv", [(1, 1), (31, 33), (128, 128), (300, 129), (4096, 4096), (1000, 257),
                                     (129, 1000), (16384, 16383), (777, 5000)])
 @pytest.mark.parametrize("causal,window", [(0, 0), (1, 0), (1, 1), (1, 100), (0, 33), (1, 128), (1, 2048), (0, 4096)])
@@ -280,11 +323,10 @@ def test_bwd_workspace_range():
     assert ws(problem(head_dim=64)) == ws(problem(head_dim=128))  # 2 bytes per pair whatever D
     assert ws(problem(head_dim=256)) == ws(problem(head_dim=128))
     assert ws(problem(head_dim=32)) == 0
-    # fp32 stages dS in fp32 over the same units: 4 bytes per pair, D <= 128
+    # fp32 stages dS in fp32 over the same units: 4 bytes per pair, every D
     band = ws(problem(head_dim=128)) - L.BWD_QUEUE_BYTES
-    for d in (32, 64, 128):
+    for d in (32, 64, 128, 256):
         assert ws(problem(head_dim=d, dtype=L.F32)) == 2 * band + L.BWD_QUEUE_BYTES
-    assert ws(problem(head_dim=256, dtype=L.F32)) == 0
     # masks keep the causal / window band of stored units (masked entries hold zeros)
     assert ws(problem(head_dim=128, doc_bounds=FAKE)) == ws(problem(head_dim=128))
     assert ws(problem(head_dim=128, block_map=FAKE, block_heads=1)) == ws(problem(head_dim=128))
