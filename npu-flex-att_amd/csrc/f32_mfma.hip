@@ -62,34 +62,59 @@ struct Cfg {
   static constexpr int DB = D / 32;               // 32-wide head-dim blocks
 };
 
-// One 32-row tile of one tensor, global -> registers -> LDS.  Rows at or past
-// `rows` read as zero (nothing past the tensor is read).
+// One 32-row tile of one tensor into an LDS tile of D + 4-float rows.
+// fetch() starts the copy, commit() completes it in the issuing thread,
+// settle() (before the barrier that publishes the tile) waits for it.  At
+// D = 256 a row is 1 KB, one direct-to-LDS load of the wave (lane l's 16
+// bytes at row offset 16 l), so the copy holds no registers; rows past the
+// tensor repeat its last row (their scores are masked, so the finite values
+// drop out).  Otherwise the copy passes through registers and rows past the
+// tensor read as zero.
 template <int D, int NW>
 struct Tile {
   using C = Cfg<D, NW>;
-  f32x4 x[C::NL];
-  __device__ __forceinline__ void load(const float* xp, int64_t xs, int r0, int rows, int tid) {
+  static constexpr bool kDirect = D == 256;
+  f32x4 x[kDirect ? 1 : C::NL];
+  float* dst = nullptr;
+  __device__ __forceinline__ void fetch(float* lds, const float* xp, int64_t xs, int r0, int rows, int tid) {
+    if constexpr (kDirect) {
+      constexpr int RPW = kTile / NW;  // rows per wave
+      const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
 #pragma unroll
-    for (int i = 0; i < C::NL; ++i) {
-      const int idx = tid + i * C::NT;
-      const int r = idx / (D / 4), c = 4 * (idx % (D / 4));
-      const int n = r0 + r;
-      const bool in = (C::N4 % C::NT == 0 || idx < C::N4) && n < rows;
-      const int nc = n < rows ? n : rows - 1;
-      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-      const f32x4 a = *(const f32x4*)(xp + (int64_t)nc * xs + c);
-      x[i] = in ? a : zero;
-    }
-  }
-  __device__ __forceinline__ void store(float* sx, int tid) const {
+      for (int i = 0; i < RPW; ++i) {
+        const int r = w * RPW + i;
+        const int n = min(r0 + r, rows - 1);
+        load_lds16(xp + (int64_t)n * xs + 4 * l, lds_addr_of(lds + r * C::P));
+      }
+    } else {
+      dst = lds;
 #pragma unroll
-    for (int i = 0; i < C::NL; ++i) {
-      const int idx = tid + i * C::NT;
-      if (C::N4 % C::NT == 0 || idx < C::N4) {
+      for (int i = 0; i < C::NL; ++i) {
+        const int idx = tid + i * C::NT;
         const int r = idx / (D / 4), c = 4 * (idx % (D / 4));
-        *(f32x4*)(sx + r * C::P + c) = x[i];
+        const int n = r0 + r;
+        const bool in = (C::N4 % C::NT == 0 || idx < C::N4) && n < rows;
+        const int nc = n < rows ? n : rows - 1;
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 a = *(const f32x4*)(xp + (int64_t)nc * xs + c);
+        x[i] = in ? a : zero;
       }
     }
+  }
+  __device__ __forceinline__ void commit(int tid) const {
+    if constexpr (!kDirect) {
+#pragma unroll
+      for (int i = 0; i < C::NL; ++i) {
+        const int idx = tid + i * C::NT;
+        if (C::N4 % C::NT == 0 || idx < C::N4) {
+          const int r = idx / (D / 4), c = 4 * (idx % (D / 4));
+          *(f32x4*)(dst + r * C::P + c) = x[i];
+        }
+      }
+    }
+  }
+  __device__ static __forceinline__ void settle() {
+    if constexpr (kDirect) wait_vmcnt<0>();
   }
 };
 
@@ -335,25 +360,26 @@ void fwd_f32_kernel(FwdArgs a) {
   Tile<D, NW> st;
   const int n_first = (kv_lo / kTile) * kTile;
   if (n_first < kv_hi) {
-    st.load(kp, a.k.ss, n_first, p.Skv, tid);
-    st.store(sK[0], tid);
-    st.load(vp, a.v.ss, n_first, p.Skv, tid);
-    st.store(sV[0], tid);
+    st.fetch(sK[0], kp, a.k.ss, n_first, p.Skv, tid);
+    st.commit(tid);
+    st.fetch(sV[0], vp, a.v.ss, n_first, p.Skv, tid);
+    st.commit(tid);
   }
+  st.settle();
   __syncthreads();
   int buf = 0;
   for (int n0 = n_first; n0 < kv_hi; n0 += kTile, buf ^= 1) {
     const bool more = n0 + kTile < kv_hi;
     const bool on = wave_live && n0 < w_hi && n0 + kTile > w_lo && (!brow || brow[n0 / kBlk] != 0);
     // next K tile in flight during this tile's S^T, next V tile during its P V
-    if (more) st.load(kp, a.k.ss, n0 + kTile, p.Skv, tid);
+    if (more) st.fetch(sK[buf ^ 1], kp, a.k.ss, n0 + kTile, p.Skv, tid);
     f32x16 s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.f;
     if (on) dsum<C::HD, C::P>(sK[buf] + l32 * C::P + h * C::HD, q, s);
     if (more) {
-      st.store(sK[buf ^ 1], tid);
-      st.load(vp, a.v.ss, n0 + kTile, p.Skv, tid);
+      st.commit(tid);
+      st.fetch(sV[buf ^ 1], vp, a.v.ss, n0 + kTile, p.Skv, tid);
     }
     if (on) {
       // scores, mask, online softmax over this lane's 16 keys and the other half's
@@ -386,7 +412,8 @@ void fwd_f32_kernel(FwdArgs a) {
       // O^T += V^T P^T: A = V[row of step r][32 db + l32], B = P^T (element r)
       rsum<C::DB, C::P>(sV[buf], l32, h, s, acc);
     }
-    if (more) st.store(sV[buf ^ 1], tid);
+    if (more) st.commit(tid);
+    st.settle();
     __syncthreads();
   }
 
@@ -502,18 +529,19 @@ void bwd_dq_f32_kernel(BwdArgs a) {
   Tile<D, NW> sk, sv;
   const int n_first = (kv_lo / kTile) * kTile;
   if (n_first < kv_hi) {
-    sk.load(kp, a.k.ss, n_first, p.Skv, tid);
-    sv.load(vp, a.v.ss, n_first, p.Skv, tid);
-    sk.store(sK[0], tid);
-    sv.store(sV[0], tid);
+    sk.fetch(sK[0], kp, a.k.ss, n_first, p.Skv, tid);
+    sv.fetch(sV[0], vp, a.v.ss, n_first, p.Skv, tid);
+    sk.commit(tid);
+    sv.commit(tid);
   }
+  sk.settle();
   __syncthreads();
   int buf = 0;
   for (int n0 = n_first; n0 < kv_hi; n0 += kTile, buf ^= 1) {
     const bool more = n0 + kTile < kv_hi;
     if (more) {
-      sk.load(kp, a.k.ss, n0 + kTile, p.Skv, tid);
-      sv.load(vp, a.v.ss, n0 + kTile, p.Skv, tid);
+      sk.fetch(sK[buf ^ 1], kp, a.k.ss, n0 + kTile, p.Skv, tid);
+      sv.fetch(sV[buf ^ 1], vp, a.v.ss, n0 + kTile, p.Skv, tid);
     }
     const bool on = wave_live && n0 < w_hi && n0 + kTile > w_lo && (!brow || brow[n0 / kBlk] != 0);
     if (on) {
@@ -537,9 +565,10 @@ void bwd_dq_f32_kernel(BwdArgs a) {
       rsum<C::DB, C::P>(sK[buf], l32, h, s, acc);
     }
     if (more) {
-      sk.store(sK[buf ^ 1], tid);
-      sv.store(sV[buf ^ 1], tid);
+      sk.commit(tid);
+      sv.commit(tid);
     }
+    sk.settle();
     __syncthreads();
   }
   if (my_m < p.Sq) {
@@ -694,13 +723,14 @@ void bwd_dkdv16_f32_kernel(BwdArgs a) {
     const float *qp, *dop;
     int m, hq;
     step_ptrs(0, qp, dop, m, hq);
-    st.load(qp, a.q.ss, m, p.Sq, tid);
-    st.store(sQ[0], tid);
-    st.load(dop, a.dout.ss, m, p.Sq, tid);
-    st.store(sO[0], tid);
+    st.fetch(sQ[0], qp, a.q.ss, m, p.Sq, tid);
+    st.commit(tid);
+    st.fetch(sO[0], dop, a.dout.ss, m, p.Sq, tid);
+    st.commit(tid);
     load_rows(m, hq);
     store_rows(0);
   }
+  st.settle();
   __syncthreads();
   int buf = 0;
   for (int u = 0; u < total; ++u, buf ^= 1) {
@@ -709,7 +739,7 @@ void bwd_dkdv16_f32_kernel(BwdArgs a) {
     int nm = 0, nhq = 0;
     if (more) {
       step_ptrs(u + 1, nqp, ndop, nm, nhq);
-      st.load(nqp, a.q.ss, nm, p.Sq, tid);
+      st.fetch(sQ[buf ^ 1], nqp, a.q.ss, nm, p.Sq, tid);
       load_rows(nm, nhq);
     }
     const int m0 = m_first + kTile * (u % nq);
@@ -729,8 +759,8 @@ void bwd_dkdv16_f32_kernel(BwdArgs a) {
       }
     }
     if (more) {
-      st.store(sQ[buf ^ 1], tid);
-      st.load(ndop, a.dout.ss, nm, p.Sq, tid);
+      st.commit(tid);
+      st.fetch(sO[buf ^ 1], ndop, a.dout.ss, nm, p.Sq, tid);
     }
     if (on) {
       const float slope = ALIBI ? p.alibi[hq] : 0.f;
@@ -769,9 +799,10 @@ void bwd_dkdv16_f32_kernel(BwdArgs a) {
       }
     }
     if (more) {
-      st.store(sO[buf ^ 1], tid);
+      st.commit(tid);
       store_rows(buf ^ 1);
     }
+    st.settle();
     __syncthreads();
   }
   if (my_n < p.Skv) {
@@ -853,21 +884,23 @@ void bwd_dq_ds_f32_kernel(BwdArgs a) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) cur[r] = nxt[r] = 0.f;
   if (kv_lo < kv_hi) {
-    st.load(kp, a.k.ss, kv_lo, p.Skv, tid);
+    st.fetch(sK[0], kp, a.k.ss, kv_lo, p.Skv, tid);
     load_ds(kv_lo, cur);
-    st.store(sK[0], tid);
+    st.commit(tid);
   }
+  st.settle();
   __syncthreads();
   int buf = 0;
   for (int n0 = kv_lo; n0 < kv_hi; n0 += kTile, buf ^= 1) {
     const bool more = n0 + kTile < kv_hi;
     if (more) {
-      st.load(kp, a.k.ss, n0 + kTile, p.Skv, tid);
+      st.fetch(sK[buf ^ 1], kp, a.k.ss, n0 + kTile, p.Skv, tid);
       load_ds(n0 + kTile, nxt);
     }
     const int kb = n0 / kDsKB;
     if (kb >= w_kb_lo && kb < w_kb_hi) rsum<C::DB, C::P>(sK[buf], l32, h, cur, acc);
-    if (more) st.store(sK[buf ^ 1], tid);
+    if (more) st.commit(tid);
+    st.settle();
     __syncthreads();
     cur = nxt;
   }
