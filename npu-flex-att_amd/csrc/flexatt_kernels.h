@@ -13,6 +13,7 @@ struct FwdArgs {
   Shape p;
   int nqt;    // number of query tiles (set by the launcher)
   int gpack;  // query heads per workgroup (set by the launcher)
+  int bstride;  // block-sparse maps: bytes per wave's block-map row in dynamic LDS (set by the launcher)
 };
 
 struct DeltaArgs {

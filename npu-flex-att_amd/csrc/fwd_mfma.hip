@@ -73,7 +73,7 @@ struct FwdCfg {
 
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
 
-template <class T, int D, bool SOFTCAP, bool ALIBI>
+template <class T, int D, bool SOFTCAP, bool ALIBI, bool BLK>
 __global__ __launch_bounds__(FwdCfg<D>::NW * 64) __attribute__((amdgpu_waves_per_eu(FwdCfg<D>::WPE, FwdCfg<D>::WPE)))
 void fwd_mfma_kernel(FwdArgs a) {
   using C = FwdCfg<D>;
@@ -146,16 +146,46 @@ void fwd_mfma_kernel(FwdArgs a) {
 
   // Block-sparse mask: this wave's row of the block map over the
   // workgroup's KV range, kept in (dynamic) LDS so that the tile loop issues
-  // no memory operation besides its tile copies.
+  // no memory operation besides its tile copies; then the list of the tiles
+  // whose block is computed for some row of the workgroup.  The tile loop
+  // walks that list (v = 0 .. nv-1 -> tile tile_of(v)); removed tiles are
+  // neither copied nor computed.  Without a map the list is [t_lo, t_hi).
   extern __shared__ unsigned char sblk[];
+  __shared__ int s_nv;
+  const int bstride = a.bstride;
+  unsigned short* tlist = (unsigned short*)(sblk + C::NW * bstride);
   const int kb_base = t_lo * C::BN / kBlk;
-  if (p.blk && t_lo < t_hi) {
+  int nv = t_hi - t_lo;
+  if (BLK && t_lo < t_hi) {
     const unsigned char* row = block_row(p, b, hq, min(mw, p.Sq - 1));
     const int nkb = (t_hi * C::BN - 1) / kBlk - kb_base + 1;
-    for (int i = lane; i < nkb; i += 64) sblk[wave * kBlkRowMax + i] = row[kb_base + i];
+    for (int i = lane; i < nkb; i += 64) sblk[wave * bstride + i] = row[kb_base + i];
+    __syncthreads();
+    if (wave == 0) {
+      int base = 0;
+      for (int t0 = t_lo; t0 < t_hi; t0 += 64) {
+        const int t = t0 + lane;
+        bool live = false;
+        if (t < t_hi) {
+          const int kb = t * C::BN / kBlk - kb_base;
+#pragma unroll
+          for (int w = 0; w < C::NW; ++w) live = live || sblk[w * bstride + kb] != 0;
+        }
+        const unsigned long long m = __builtin_amdgcn_ballot_w64(live);
+        if (live) tlist[base + __builtin_popcountll(m & ((1ull << lane) - 1))] = (unsigned short)(t - t_lo);
+        base += __builtin_popcountll(m);
+      }
+      if (lane == 0) s_nv = base;
+    }
+    __syncthreads();
+    nv = __builtin_amdgcn_readfirstlane(s_nv);
   }
+  auto tile_of = [&](int v) -> int {
+    if constexpr (BLK) return t_lo + __builtin_amdgcn_readfirstlane((int)tlist[v]);
+    else return t_lo + v;
+  };
   // whether the 128 x 128 block of this wave's rows and KV row n0 is computed
-  auto block_live = [&](int n0) { return !p.blk || sblk[wave * kBlkRowMax + n0 / kBlk - kb_base] != 0; };
+  auto block_live = [&](int n0) { return !BLK || sblk[wave * bstride + n0 / kBlk - kb_base] != 0; };
 
   // Direct global -> LDS copy of tile t into stage st: E 1 KB loads per
   // tensor per wave; lane l of load e covers physical chunk q of the tile.
@@ -323,11 +353,12 @@ void fwd_mfma_kernel(FwdArgs a) {
     // phase.  (Moving the packing and row sums into the MFMA phase, or the
     // copies into the VALU phase, measured slower: the two phases are about
     // equally long.)
-    // Tile u lives in stage (u - t_lo) % 4 from its copy (issued at the start
-    // of M(u-2)) until B's M(u+1) has read V(u); the copy of tile u+4 into
-    // that stage is issued at M(u+2), after the barrier that ends B's M(u+1).
+    // The v-th tile of the walk lives in stage v % 4 from its copy (issued at
+    // the start of M(v-2)) until B's M(v+1) has read its V; the copy of tile
+    // v+4 into that stage is issued at M(v+2), after the barrier that ends
+    // B's M(v+1).
     const int grp = wave >> 2;
-    // Tile copies are issued in tile order, one per M phase, past the last
+    // Tile copies are issued in walk order, one per M phase, past the last
     // tile as redundant copies of it into a free stage, so that each wave
     // always has exactly one copy in flight beyond the tile it needs next and
     // every wait is vmcnt(2E) (vector memory operations complete in order, a
@@ -342,13 +373,20 @@ void fwd_mfma_kernel(FwdArgs a) {
     }
     const int64_t kstep = (int64_t)C::BN * a.k.ss * (int64_t)sizeof(T);
     const int64_t vstep = (int64_t)C::BN * a.v.ss * (int64_t)sizeof(T);
+    // copy cursors: stepped tile by tile without a map, set from the list with one
     const char* kcur = (const char*)(kp + (int64_t)t_lo * C::BN * a.k.ss);
     const char* vcur = (const char*)(vp + (int64_t)t_lo * C::BN * a.v.ss);
-    int next_t = t_lo;
+    int next_v = 0;
     auto issue_next = [&]() {
-      const int t = next_t++;
-      const int st = (t - t_lo) & 3;
-      if (t < t_hi && (t + 1) * C::BN <= p.Skv) {
+      const int v = next_v++;
+      const int st = v & 3;
+      int t = t_lo + v;
+      if constexpr (BLK) {
+        t = tile_of(min(v, nv - 1));
+        kcur = (const char*)kp + t * kstep;
+        vcur = (const char*)vp + t * vstep;
+      }
+      if (v < nv && (t + 1) * C::BN <= p.Skv) {
         const unsigned dst = lds0 + st * 2 * C::TILEB + wave * C::E * 1024;
 #pragma unroll
         for (int e = 0; e < C::E; ++e) {
@@ -358,7 +396,8 @@ void fwd_mfma_kernel(FwdArgs a) {
         kcur += kstep;
         vcur += vstep;
       } else {
-        issue(min(t, t_hi - 1), st);  // KV tail (rows clamped to Skv - 1) or redundant copy
+        // KV tail (rows clamped to Skv - 1) or a redundant copy of the last tile
+        issue(BLK ? t : min(t, t_hi - 1), st);
       }
     };
     auto wait_tile = [&]() { wait_vmcnt<2 * C::E>(); };
@@ -504,53 +543,53 @@ void fwd_mfma_kernel(FwdArgs a) {
       }
     };
 
-    if (t_lo < t_hi) {
-      issue_next();  // t_lo
-      issue_next();  // t_lo + 1
+    if (nv > 0) {
+      issue_next();  // v = 0
+      issue_next();  // v = 1
       wait_tile();
       __syncthreads();
       if (grp) __syncthreads();  // second half starts one phase late
-      issue_next();  // t_lo + 2
+      issue_next();  // v = 2
       mphase(0, 0, false, true);
       wait_tile();
       __syncthreads();
       pin_s();
-      for (int t = t_lo; t + 1 < t_hi; ++t) {
-        softmax(t * C::BN);
+      for (int v = 0; v + 1 < nv; ++v) {
+        softmax(tile_of(v) * C::BN);
         wait_tile();
         __syncthreads();
         pin_p();
         // the MFMA phase issues ahead of the other wave's softmax on the SIMD
         // (measured 1-1.5% faster; raising the softmax wave instead is slower)
         __builtin_amdgcn_s_setprio(1);
-        issue_next();  // t + 3
-        mphase((t - t_lo) & 3, (t + 1 - t_lo) & 3, true, true);
+        issue_next();  // v + 3
+        mphase(v & 3, (v + 1) & 3, true, true);
         __builtin_amdgcn_s_setprio(0);
         wait_tile();
         __syncthreads();
         pin_s();
       }
-      softmax((t_hi - 1) * C::BN);
+      softmax(tile_of(nv - 1) * C::BN);
       wait_tile();
       __syncthreads();
       pin_p();
-      mphase((t_hi - 1 - t_lo) & 3, 0, true, false);
+      mphase((nv - 1) & 3, 0, true, false);
       wait_vmcnt<0>();  // no copy may land after the workgroup's LDS is released
       __syncthreads();
       if (!grp) __syncthreads();  // first half: match the second's count
     }
   } else {
-    if (t_lo < t_hi) issue(t_lo, 0);
-    if (t_lo + 1 < t_hi) issue(t_lo + 1, 1);
+    if (nv > 0) issue(tile_of(0), 0);
+    if (nv > 1) issue(tile_of(1), 1);
     int st = 0;
-    for (int t = t_lo; t < t_hi; ++t) {
-      if (t + 1 < t_hi) wait_vmcnt<2 * C::E>();
+    for (int v = 0; v < nv; ++v) {
+      if (v + 1 < nv) wait_vmcnt<2 * C::E>();
       else wait_vmcnt<0>();
       __syncthreads();
-      if (t + 2 < t_hi) issue(t + 2, st == 0 ? 2 : st - 1);
+      if (v + 2 < nv) issue(tile_of(v + 2), st == 0 ? 2 : st - 1);
       const char* sK = smem + st * 2 * C::TILEB;
       const char* sV = sK + C::TILEB;
-      const int n0 = t * C::BN;
+      const int n0 = tile_of(v) * C::BN;
       // Per element masking only on tiles that cut the causal diagonal, the
       // window edge or the KV tail for some row of this wave.
       const bool need_mask = (n0 + C::BN > p.Skv) || (p.causal && n0 + C::BN - 1 > mw) ||
@@ -608,11 +647,21 @@ hipError_t launch_fwd_mfma(const FwdArgs& a, hipStream_t st) {
   x.nqt = (a.p.Sq + bmh - 1) / bmh;
   const dim3 grid(x.nqt * (a.p.G / x.gpack) * a.p.B * a.p.Hkv), block(C::NW * 64);
   const bool sc = a.p.cap > 0.f, al = a.p.alibi != nullptr;
-  const size_t dyn = a.p.blk ? (size_t)C::NW * kBlkRowMax : 0;  // block-map rows
-  if (sc && al) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true, true>), grid, block, dyn, st, x);
-  else if (sc) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true, false>), grid, block, dyn, st, x);
-  else if (al) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false, true>), grid, block, dyn, st, x);
-  else hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false, false>), grid, block, dyn, st, x);
+  // block-sparse maps: each wave's block-map row, then the workgroup's tile list
+  x.bstride = (a.p.blk_nk + 3) & ~3;
+  const int tiles = (a.p.Skv + C::BN - 1) / C::BN;
+  const size_t dyn = a.p.blk ? (size_t)C::NW * x.bstride + 2 * (size_t)(tiles + 2) : 0;
+  if (a.p.blk) {
+    if (sc && al) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true, true, true>), grid, block, dyn, st, x);
+    else if (sc) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true, false, true>), grid, block, dyn, st, x);
+    else if (al) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false, true, true>), grid, block, dyn, st, x);
+    else hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false, false, true>), grid, block, dyn, st, x);
+  } else {
+    if (sc && al) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true, true, false>), grid, block, 0, st, x);
+    else if (sc) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true, false, false>), grid, block, 0, st, x);
+    else if (al) hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false, true, false>), grid, block, 0, st, x);
+    else hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false, false, false>), grid, block, 0, st, x);
+  }
   return hipGetLastError();
 }
 
