@@ -92,7 +92,7 @@ struct KvCfg {
 
 // PASS 0: dV and dK together; PASS 1: dV only; PASS 2: dK only (with the
 // staged dS when DS).
-template <class T, int D, bool SOFTCAP, bool ALIBI, bool DS, int PASS>
+template <class T, int D, bool SOFTCAP, bool ALIBI, bool DS, int PASS, bool BLK>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(KvCfg<D>::WPE, KvCfg<D>::WPE)))
 void bwd_kv_kernel(BwdArgs a) {
   using C = KvCfg<D>;
@@ -143,7 +143,7 @@ void bwd_kv_kernel(BwdArgs a) {
   if (p.window > 0) q_hi = min(q_hi, n0 + C::BKV + p.window);  // q - kv <= W
   const int qt_lo = q_lo / C::BM;
   const int nqt = q_hi > q_lo ? (q_hi + C::BM - 1) / C::BM - qt_lo : 0;
-  const int ntile = p.G * nqt;
+  int ntile = p.G * nqt;
   // Tile order: the G heads of a query tile consecutively; the first round
   // of workgroups (one per CU) walks the query tiles from the last one down,
   // later ones (causal) from the diagonal up.  The first round starts
@@ -155,6 +155,39 @@ void bwd_kv_kernel(BwdArgs a) {
   const int qt_top = qt_lo + nqt - 1;
   const bool up = p.causal && slot >= a.nstatic;
   const int qt0 = up ? qt_lo : qt_top, qt_end = up ? qt_top : qt_lo, qstep = up ? 1 : -1;
+
+  // Block-sparse maps (BLK): the query tiles, in walk order, whose 128 x 128
+  // block with this KV block is computed for some head of the group; the walk
+  // visits only those (nlive of them), every head of each.  Heads whose own
+  // block is removed in a listed tile skip their S-wave work (below).
+  extern __shared__ unsigned short qlist[];
+  __shared__ int s_nlive;
+  int nlive = nqt;
+  if constexpr (BLK) {
+    if (wave == 0) {
+      const int kbc = min(n0, p.Skv - 1) / kBlk;
+      const int nh = p.blk_h > 1 ? p.G : 1;  // heads with a row of their own
+      int base = 0;
+      for (int i0 = 0; i0 < nqt; i0 += 64) {
+        const int i = i0 + lane;
+        bool live = false;
+        if (i < nqt) {
+          const int qt = qt0 + i * qstep;
+          for (int g = 0; g < nh && !live; ++g)
+            live = block_row(p, b, hk * p.G + g, min(qt * C::BM, p.Sq - 1))[kbc] != 0;
+        }
+        const unsigned long long m = __builtin_amdgcn_ballot_w64(live);
+        if (live) qlist[base + __builtin_popcountll(m & ((1ull << lane) - 1))] = (unsigned short)(qt0 + i * qstep);
+        base += __builtin_popcountll(m);
+      }
+      if (lane == 0) s_nlive = base;
+    }
+    __syncthreads();
+    nlive = __builtin_amdgcn_readfirstlane(s_nlive);
+  }
+  // query tile of walk position i (BLK), the head of step u being u % G
+  auto qt_at = [&](int i) -> int { return __builtin_amdgcn_readfirstlane((int)qlist[i]); };
+  if constexpr (BLK) ntile = p.G * nlive;
 
   // Lane-constant LDS byte offsets of the row reads (S-wave) and the
   // transpose reads (KV-wave) within a tile.
@@ -228,7 +261,7 @@ void bwd_kv_kernel(BwdArgs a) {
       return block_row(p, b, hk * p.G + g, min(qt * C::BM, p.Sq - 1))[min(kw0, p.Skv - 1) / kBlk];
     };
     int blk_next = 1;
-    if (p.blk && ntile > 0) blk_next = blk_byte(0, qt0);
+    if (p.blk && ntile > 0) blk_next = blk_byte(0, BLK ? qt_at(0) : qt0);
 
     __syncthreads();  // prologue: tile 0 landed
     for (int u = 0; u <= ntile; ++u) {
@@ -238,8 +271,15 @@ void bwd_kv_kernel(BwdArgs a) {
       bool live = true;
       if (p.blk && act) {
         live = __builtin_amdgcn_readfirstlane(blk_next) != 0;
-        const int ng = cg + 1 == p.G ? 0 : cg + 1, nqt = cg + 1 == p.G ? cqt + qstep : cqt;
-        if (u + 1 < ntile) blk_next = blk_byte(ng, nqt);
+        int ng, nq;
+        if constexpr (BLK) {
+          ng = (u + 1) % p.G;
+          nq = u + 1 < ntile ? qt_at((u + 1) / p.G) : 0;
+        } else {
+          ng = cg + 1 == p.G ? 0 : cg + 1;
+          nq = cg + 1 == p.G ? cqt + qstep : cqt;
+        }
+        if (u + 1 < ntile) blk_next = blk_byte(ng, nq);
       }
       // ---- M(u): S = Q K^T, DP = Delta - dO V^T of tile u; LSE reads ------
       if (act && live) {
@@ -295,6 +335,10 @@ void bwd_kv_kernel(BwdArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       // ---- V(u): P, dS of tile u -> exchange buffer u & 1 -----------------
       if (act) {
+        if constexpr (BLK) {  // tile u of the list walk
+          cg = u % p.G;
+          cqt = qt_at(u / p.G);
+        }
         const int hq = hk * p.G + cg;
         const int m0 = cqt * C::BM;
         const float sl = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
@@ -408,15 +452,18 @@ void bwd_kv_kernel(BwdArgs a) {
     const int64_t owrap = (int64_t)qstep * C::BM * a.dout.ss * (int64_t)sizeof(T) - (int64_t)(p.G - 1) * oh;
     const int64_t lwrap = (int64_t)qstep * C::BM - (int64_t)(p.G - 1) * p.Sq;
     int is_g = 0, is_qt = qt0;  // next tile to copy (head, query tile)
+    if constexpr (BLK) is_qt = nlive > 0 ? qt_at(0) : qt0;
     const char *qcur, *ocur;
     const float* lcur;  // LSE (lanes 0-7) or Delta (lanes 8-15) row m0
-    {
-      const int hq = hk * p.G;
-      const int64_t m0 = (int64_t)qt0 * C::BM;
+    auto point = [&](int g, int qt) {
+      const int hq = hk * p.G + g;
+      const int64_t m0 = (int64_t)qt * C::BM;
       qcur = (const char*)((const T*)a.q.data + b * a.q.sb + hq * a.q.sh + m0 * a.q.ss);
       ocur = (const char*)((const T*)a.dout.data + b * a.dout.sb + hq * a.dout.sh + m0 * a.dout.ss);
       lcur = (lane < 8 ? a.lse : a.delta) + (int64_t)(b * p.Hq + hq) * p.Sq + m0;
-    }
+    };
+    point(0, is_qt);
+    int cu = 0;  // BLK: walk step of the next copy
     bool tail = false;
     auto prep = [&]() {  // per-lane offsets for the query tile is_qt
       const int m0 = is_qt * C::BM;
@@ -438,7 +485,18 @@ void bwd_kv_kernel(BwdArgs a) {
       }
     };
     auto advance = [&]() {  // past the end the last tile is copied again
-      if (is_g < p.G - 1 || is_qt != qt_end) {
+      if constexpr (BLK) {
+        if (cu + 1 < ntile) {
+          ++cu;
+          const int qt = qt_at(cu / p.G);
+          is_g = cu % p.G;
+          point(is_g, qt);
+          if (qt != is_qt) {
+            is_qt = qt;
+            prep();
+          }
+        }
+      } else if (is_g < p.G - 1 || is_qt != qt_end) {
         if (++is_g == p.G) {
           is_g = 0;
           is_qt += qstep;
@@ -493,15 +551,21 @@ void bwd_kv_kernel(BwdArgs a) {
     // ds_qt, this KV block), moved per tile with the band counts of the query
     // tiles it passes.
     int ds_g = 0, ds_qt = qt0;
+    if constexpr (BLK) ds_qt = nlive > 0 ? qt_at(0) : qt0;
     int xtr = 0;
     char* dsp = nullptr;
+    // this lane's 16 bytes of the unit of (head hk G + g, query tile qt, this KV block)
+    auto ds_at = [&](int g, int qt) {
+      const int64_t unit = (int64_t)(b * p.Hq + hk * p.G + g) * a.ds_head +
+                           ds_tile_offset(qt, p.causal, p.window, nkb) + kb - ds_kb_lo(qt, p.window, nkb);
+      return a.ds + unit * kDsUnitB + (2 * pr) * 1024 + lane * 16;
+    };
+    int su = 0;  // BLK: walk step of the next dS store
     if constexpr (DS) {
       const int aq = 4 * ((lane >> 4) & 1) + (lane & 3);
       const int jr = 4 * (lane >> 5) + ((lane & 15) >> 2);
       xtr = C::XOFF + pr * C::XB + (SLOT_DS + (aq >> 2)) * 1024 + (((aq & 1) << 5) + jr) * 16 + 8 * ((aq >> 1) & 1);
-      const int64_t unit = (int64_t)(b * p.Hq + hk * p.G) * a.ds_head +
-                           ds_tile_offset(qt0, p.causal, p.window, nkb) + kb - ds_kb_lo(qt0, p.window, nkb);
-      dsp = a.ds + unit * kDsUnitB + (2 * pr) * 1024 + lane * 16;
+      dsp = ds_at(0, ds_qt);
     }
 
     if (ntile > 0) {
@@ -525,6 +589,10 @@ void bwd_kv_kernel(BwdArgs a) {
       for (int f = 0; f < 2; ++f)
         __builtin_nontemporal_store(__builtin_bit_cast(i32x4, cat_tr<V8>(st4[2 * f], st4[2 * f + 1])),
                                     (i32x4*)(dsp + f * 1024));
+      if constexpr (BLK) {
+        if (++su < ntile) dsp = ds_at(su % p.G, qt_at(su / p.G));
+        return;
+      }
       int64_t step;  // in units
       if (++ds_g == p.G) {
         // first head of the next query tile t: the unit index moves by
@@ -656,10 +724,21 @@ hipError_t launch_kv(const BwdArgs& a, hipStream_t st) {
     constexpr int PS = decltype(pass_c)::value;
     constexpr bool DSP = DS && PS != 1;
     x.queue = a.queue ? a.queue + (PS == 2 ? 1 : 0) : nullptr;  // one counter per launch
-    if (sc && al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, true, DSP, PS>), grid, block, 0, st, x);
-    else if (sc) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, false, DSP, PS>), grid, block, 0, st, x);
-    else if (al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, true, DSP, PS>), grid, block, 0, st, x);
-    else hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, false, DSP, PS>), grid, block, 0, st, x);
+    // block-sparse maps: the walk list of live query tiles in dynamic LDS
+    // (when it fits beside the tile stages; otherwise removed tiles are walked
+    // and only their S-wave work is skipped)
+    const size_t dyn = 2 * (size_t)((a.p.Sq + C::BM - 1) / C::BM + 2);
+    if (a.p.blk && C::LDSB + dyn <= 160 * 1024) {
+      if (sc && al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, true, DSP, PS, true>), grid, block, dyn, st, x);
+      else if (sc) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, false, DSP, PS, true>), grid, block, dyn, st, x);
+      else if (al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, true, DSP, PS, true>), grid, block, dyn, st, x);
+      else hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, false, DSP, PS, true>), grid, block, dyn, st, x);
+      return hipGetLastError();
+    }
+    if (sc && al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, true, DSP, PS, false>), grid, block, 0, st, x);
+    else if (sc) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, false, DSP, PS, false>), grid, block, 0, st, x);
+    else if (al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, true, DSP, PS, false>), grid, block, 0, st, x);
+    else hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, false, DSP, PS, false>), grid, block, 0, st, x);
     return hipGetLastError();
   };
   if constexpr (C::PASSES) {
