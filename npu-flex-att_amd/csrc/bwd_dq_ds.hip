@@ -61,7 +61,7 @@ struct DqsCfg {
   static_assert(KSTAGES * KTILEB <= 128 * 1024, "LDS");
 };
 
-template <class T, int D>
+template <class T, int D, bool BLK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void bwd_dq_ds_kernel(BwdArgs a) {
   using C = DqsCfg<D>;
@@ -164,6 +164,43 @@ void bwd_dq_ds_kernel(BwdArgs a) {
   }
   auto live = [&](int c, int s) { return !p.blk || myblk[c * kBlkRowMax + s / SPB - kb0] != 0; };
 
+  // Block-sparse maps (BLK): the sub-blocks some slot of the workgroup
+  // computes (inside its band, block not removed), in order; the walk visits
+  // only those (step i: sub-block g_lo + slist[i]).
+  unsigned short* slist = (unsigned short*)(sblk + C::NW * C::NSL * kBlkRowMax);
+  __shared__ int s_nlive;
+  int nlive = nsub;
+  if constexpr (BLK) {
+    __syncthreads();  // every wave's block-map rows are in LDS
+    if (wave == 0) {
+      int base = 0;
+      for (int i0 = 0; i0 < nsub; i0 += 64) {
+        const int sb = g_lo + i0 + lane;
+        bool any = false;
+        if (i0 + lane < nsub) {
+          for (int v = 0; v < C::NW && !any; ++v)
+            for (int c = 0; c < C::NSL && !any; ++c) {
+              int hq, t, lo, hi;
+              slot_of(v, c, hq, t);
+              band_of(t, lo, hi);
+              any = sb >= lo && sb < hi && sblk[(v * C::NSL + c) * kBlkRowMax + sb / SPB - kb0] != 0;
+            }
+        }
+        const unsigned long long m = __builtin_amdgcn_ballot_w64(any);
+        if (any) slist[base + __builtin_popcountll(m & ((1ull << lane) - 1))] = (unsigned short)(i0 + lane);
+        base += __builtin_popcountll(m);
+      }
+      if (lane == 0) s_nlive = base;
+    }
+    __syncthreads();
+    nlive = __builtin_amdgcn_readfirstlane(s_nlive);
+  }
+  // sub-block of walk step i (i < nlive)
+  auto sub_at = [&](int i) -> int {
+    if constexpr (BLK) return g_lo + __builtin_amdgcn_readfirstlane((int)slist[i]);
+    else return g_lo + i;
+  };
+
   // K copies: chunk q = (wave EK + e) 64 + lane of the sub-block, row q / CPR,
   // at its swizzled chunk (the dual-use swizzle of the backward tiles).
   int krow[C::EK], kchk[C::EK];
@@ -174,8 +211,8 @@ void bwd_dq_ds_kernel(BwdArgs a) {
     kchk[e] = swz_dual_inv<C::CPR>(krow[e], q % C::CPR);
   }
   const unsigned lds0 = lds_addr_of(smem);
-  auto issue_k = [&](int i) {  // K rows of sub-block g_lo + i (clamped) into stage i % KSTAGES
-    const int s = min(g_lo + i, g_hi - 1);
+  auto issue_k = [&](int i) {  // K rows of walk step i (clamped to the last) into stage i % KSTAGES
+    const int s = BLK ? sub_at(min(i, nlive - 1)) : min(g_lo + i, g_hi - 1);
     const unsigned sb = lds0 + (i & (C::KSTAGES - 1)) * C::KTILEB;
 #pragma unroll
     for (int e = 0; e < C::EK; ++e) {
@@ -185,7 +222,7 @@ void bwd_dq_ds_kernel(BwdArgs a) {
   };
   // dS of sub-block g_lo + i for the wave's slots into buf (NSL x KS operands)
   auto issue_ds = [&](int i, i32x4 (&buf)[C::NDS]) {
-    const int s = g_lo + i;
+    const int s = i < nlive ? sub_at(i) : g_hi;  // past the end: outside every band (cached dummy loads)
 #pragma unroll
     for (int c = 0; c < C::NSL; ++c) {
       const bool in = s >= s_lo[c] && s < s_hi[c] && live(c, s);
@@ -240,7 +277,7 @@ void bwd_dq_ds_kernel(BwdArgs a) {
     __syncthreads();  // every wave's K copies of i landed; stage (i - 1) % 4 is free
     issue_k(i + C::KAHEAD);
     issue_ds(i + C::DAHEAD, dsb[BN]);
-    const int s = g_lo + i;
+    const int s = sub_at(i);
     bool on[C::NSL];
 #pragma unroll
     for (int c = 0; c < C::NSL; ++c) on[c] = s >= s_lo[c] && s < s_hi[c] && live(c, s);
@@ -267,7 +304,7 @@ void bwd_dq_ds_kernel(BwdArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  if (nsub > 0) {
+  if (nlive > 0) {
     // prologue in the steady-state issue order: K 0, K 1, dS 0, K 2, dS 1
     issue_k(0);
     issue_k(1);
@@ -275,13 +312,13 @@ void bwd_dq_ds_kernel(BwdArgs a) {
     issue_k(2);
     issue_ds(1, dsb[1]);
     int i = 0;
-    for (; i + 3 <= nsub; i += 3) {
+    for (; i + 3 <= nlive; i += 3) {
       step(i, std::integral_constant<int, 0>{});
       step(i + 1, std::integral_constant<int, 1>{});
       step(i + 2, std::integral_constant<int, 2>{});
     }
-    if (i < nsub) step(i, std::integral_constant<int, 0>{});
-    if (i + 1 < nsub) step(i + 1, std::integral_constant<int, 1>{});
+    if (i < nlive) step(i, std::integral_constant<int, 0>{});
+    if (i + 1 < nlive) step(i + 1, std::integral_constant<int, 1>{});
     // The copies and loads past the end land before anything else runs: the
     // loads' destination registers are named in the waits, so the compiler
     // keeps them allocated (a register reused while a load into it is in
@@ -317,8 +354,14 @@ hipError_t launch_dq_ds(const BwdArgs& a, hipStream_t st) {
   const int nqb = (nqt + nq - 1) / nq;
   x.ntiles = (nqb << 8) | nh;
   const dim3 grid(nqb * (a.p.G / nh) * a.p.B * a.p.Hkv), block(C::NW * 64);
-  const size_t dyn = a.p.blk ? (size_t)C::NW * C::NSL * kBlkRowMax : 0;  // block-map rows of the slots
-  hipLaunchKernelGGL((bwd_dq_ds_kernel<T, D>), grid, block, dyn, st, x);
+  // block-sparse maps: block-map rows of the slots, then the sub-block walk list
+  const int nsb = (a.p.Skv + C::SB - 1) / C::SB;
+  if (a.p.blk) {
+    const size_t dyn = (size_t)C::NW * C::NSL * kBlkRowMax + 2 * (size_t)(nsb + 2);
+    hipLaunchKernelGGL((bwd_dq_ds_kernel<T, D, true>), grid, block, dyn, st, x);
+  } else {
+    hipLaunchKernelGGL((bwd_dq_ds_kernel<T, D, false>), grid, block, 0, st, x);
+  }
   return hipGetLastError();
 }
 
