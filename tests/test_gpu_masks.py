@@ -51,6 +51,10 @@ CASES = {
     "fp16_d256_blocks": (torch.float16, 256, 1, 2, 2, 300, 300, dict(causal=True, blocks=(6, 2, None))),
     "fp32_d64_prefix_doc": (torch.float32, 64, 1, 4, 2, 300, 300, dict(causal=True, prefix=[120], doc=[50, 150, 100])),
     "fp32_d128_blocks": (torch.float32, 128, 1, 2, 1, 260, 260, dict(blocks=(7, 2, 1))),
+    # walk lists longer than one 64-lane compaction round in every kernel
+    # (66 forward KV tiles, 132 dK/dV query tiles, 66 dQ sub-blocks)
+    "bf16_d128_blocks_long": (torch.bfloat16, 128, 1, 2, 1, 4224, 4224, dict(causal=True, blocks=(8, 2, None))),
+    "fp16_d64_blocks_long_shared": (torch.float16, 64, 1, 2, 2, 4160, 4200, dict(blocks=(9, 1, 3))),
 }
 
 
