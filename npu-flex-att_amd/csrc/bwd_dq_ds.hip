@@ -148,9 +148,9 @@ void bwd_dq_ds_kernel(BwdArgs a) {
 
   // Block-sparse maps: the block-map row of each of this wave's slots over
   // the workgroup's KV blocks, in (dynamic) LDS, so that the loop issues no
-  // memory operation besides its own loads; a slot skips the MFMAs of
-  // sub-blocks in removed blocks and loads a cached address instead of their
-  // (zero) dS.
+  // memory operation besides its own loads; in a walked sub-block, a slot
+  // whose block is removed skips its MFMAs and loads a cached address
+  // instead of its dS (the dK/dV kernel does not store removed units).
   extern __shared__ unsigned char sblk[];
   constexpr int SPB = kBlk / C::SB;  // sub-blocks per block
   const int kb0 = g_lo / SPB, nkbw = nsub > 0 ? (g_hi - 1) / SPB - kb0 + 1 : 0;

@@ -255,8 +255,10 @@ void bwd_kv_kernel(BwdArgs a) {
     int sc = 0;               // its stage
     // Block-sparse maps: the byte of tile u's 128 x 128 block, loaded one
     // step ahead (the S-wave has no other memory operation in flight, so the
-    // wait at its use is for this load alone).  A removed tile skips the
-    // S-wave's MFMAs and VALU work: its P and dS are written as zeros.
+    // wait at its use is for this load alone).  A removed tile that is still
+    // walked (a listed tile whose block is removed for this head, or a walk
+    // without the list) skips the S-wave's MFMAs and VALU work: its P and dS
+    // are written as zeros.
     auto blk_byte = [&](int g, int qt) -> int {
       return block_row(p, b, hk * p.G + g, min(qt * C::BM, p.Sq - 1))[min(kw0, p.Skv - 1) / kBlk];
     };

@@ -27,10 +27,12 @@
 //  * Only tiles that straddle a mask edge or the KV tail evaluate the mask per
 //    element; fully masked blocks of such tiles run the same instructions
 //    with P = 0 (one straight path keeps the accumulators in place).
-//  * Block-sparse maps: a wave skips the softmax of tiles in removed
-//    128 x 128 blocks of its rows and feeds P = 0 to their PV MFMAs (a
-//    branch around the MFMA phase costs the ping-pong loop its register
-//    budget); the 4-wave form (D = 256) skips such tiles entirely.
+//  * Block-sparse maps: the workgroup walks only the KV tiles whose
+//    128 x 128 block is computed for some of its rows (a list built in LDS
+//    at the start); in a listed tile, a wave whose own block is removed
+//    skips the softmax and feeds P = 0 to its PV MFMAs (a branch around the
+//    MFMA phase costs the ping-pong loop its register budget); the 4-wave
+//    form (D = 256) skips the whole tile for that wave.
 #include "flexatt_device.h"
 #include "flexatt_kernels.h"
 
