@@ -186,9 +186,10 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
  * the dQ kernel forms dQ = scale * dS K from them instead of recomputing S
  * and dP.  The workspace holds 2 bytes (fp32: 4 bytes) per attended (query
  * row, KV row) pair of each query head, in 32 x 128 units over the causal /
- * window band (interval
- * and block masks keep that band; their masked pairs hold zeros),
- * followed by FLEXATT_BWD_QUEUE_BYTES of work-queue counters:
+ * window band (interval and block masks keep that band; masked pairs hold
+ * zeros, and the units of removed 128 x 128 blocks are neither written nor
+ * read by the fp16/bf16 kernels), followed by FLEXATT_BWD_QUEUE_BYTES of
+ * work-queue counters:
  * flexatt_bwd_workspace(p) bytes in all (0: the problem is outside this
  * range), 16-byte aligned, not zeroed, reusable once the call's work on
  * `stream` is done.  Same results as flexatt_bwd up to fp32 summation
