@@ -126,15 +126,14 @@ Shape make_shape(const flexatt_problem* p) {
 View view(const flexatt_tensor* t) { return View{t->data, t->stride_b, t->stride_h, t->stride_s}; }
 MutView mview(const flexatt_tensor* t) { return MutView{t->data, t->stride_b, t->stride_h, t->stride_s}; }
 
-// [dtype][head index]; fp32 on the fp32 matrix cores except the recomputing
-// dQ at D = 256 (vector ALU kernel)
+// [dtype][head index]
 const FwdLauncher kFwd[3][4] = {
     {fwd_f32_d32, fwd_f32_d64, fwd_f32_d128, fwd_f32_d256},
     {fwd_mfma_f16_d32, fwd_mfma_f16_d64, fwd_mfma_f16_d128, fwd_mfma_f16_d256},
     {fwd_mfma_bf16_d32, fwd_mfma_bf16_d64, fwd_mfma_bf16_d128, fwd_mfma_bf16_d256},
 };
 const BwdLauncher kDq[3][4] = {
-    {bwd_dq_f32_d32, bwd_dq_f32_d64, bwd_dq_f32_d128, bwd_dq_simt_f32_d256},
+    {bwd_dq_f32_d32, bwd_dq_f32_d64, bwd_dq_f32_d128, bwd_dq_f32_d256},
     {bwd_dq_mfma_f16_d32, bwd_dq_mfma_f16_d64, bwd_q_f16_d128, bwd_dq_mfma_f16_d256},
     {bwd_dq_mfma_bf16_d32, bwd_dq_mfma_bf16_d64, bwd_q_bf16_d128, bwd_dq_mfma_bf16_d256},
 };

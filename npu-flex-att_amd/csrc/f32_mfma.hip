@@ -1,5 +1,5 @@
-// fp32 flash attention on the fp32 matrix cores (v_mfma_f32_32x32x2_f32):
-// forward, dQ and dK/dV for fp32 inputs.
+// fp32 flash attention on the fp32 matrix cores: forward, dQ (from the
+// staged dS, or recomputing S and dP) and dK/dV for fp32 inputs.
 //
 // The reference accepts fp32 tensors on the same entry points
 // (test/test_supplementary.py:55-63; the fp32 suites of
@@ -12,24 +12,28 @@
 // sliding window, soft-cap, ALiBi, interval and block masks, and the GQA
 // group sum inside dK/dV.
 //
-// MFMA 32x32x2 fp32 lane layout (K = 2: one value per lane per operand):
-//   A operand  lane l holds A[row = l%32][k = l/32]
-//   B operand  lane l holds B[k = l/32][col = l%32]
-//   C/D        acc[4*i + j] = C[row = 8*i + 4*(l/32) + j][col = l%32]
-// A product over the head dim runs as D/2 MFMAs; wave half h takes
-// d = h*D/2 + s at step s, so that each lane reads its operand rows as
-// contiguous 16-byte groups.  A product over 32 rows (P V, dS K) takes at
-// step r the rows 8*(r/4) + 4h + r%4 -- exactly the rows
-// whose scores lane half h holds in accumulator element r, so the scores
-// feed the B operand from their own registers.
+// Two MFMA shapes, one operand value per lane per instruction:
+//  * v_mfma_f32_32x32x2_f32 (the forward and the dQ from the staged dS):
+//      A operand  lane l holds A[row = l%32][k = l/32]
+//      B operand  lane l holds B[k = l/32][col = l%32]
+//      C/D        acc[4*i + j] = C[row = 8*i + 4*(l/32) + j][col = l%32]
+//    A product over the head dim runs as D/2 MFMAs; wave half h takes
+//    d = h*D/2 + s at step s, so that each lane reads its operand rows as
+//    contiguous 16-byte groups.  A product over 32 rows (P V, dS K) takes at
+//    step r the rows 8*(r/4) + 4h + r%4 -- exactly the rows whose scores
+//    lane half h holds in accumulator element r, so the scores feed the B
+//    operand from their own registers.
+//  * v_mfma_f32_16x16x4_f32 (dK/dV and the recomputing dQ, 16 rows per
+//    wave, half the per-lane state): layout and step order given with it
+//    below.
 //
 // Forward and dQ keep the query rows as the accumulator columns
 // (S^T = K Q^T, one query row per lane); dK/dV keeps the KV rows as columns
-// (S = Q K^T, one KV row per lane, on the 16 x 16 x 4 MFMA, whose layout is
-// given with it below).  K/V (or Q/dO) tiles of 32 rows pass
-// through registers into a double-buffered LDS tile with rows padded to
-// D + 4 floats (16-byte row reads and 4-byte column reads both without bank
-// conflicts), one barrier per tile.
+// (S = Q K^T, one KV row per lane).  K/V (or Q/dO) tiles of 32 rows pass
+// through registers (at D = 256: one direct-to-LDS load per row) into a
+// double-buffered LDS tile with rows padded to D + 4 floats (16-byte row
+// reads and 4-byte column reads both without bank conflicts), one barrier
+// per tile.
 #include "flexatt_device.h"
 #include "flexatt_kernels.h"
 
@@ -135,28 +139,6 @@ __device__ __forceinline__ void dsum(const float* t, const float (&b)[HD], f32x1
     __builtin_amdgcn_sched_barrier(0);
   }
 }
-// Two such sums over the same rows of two tiles.
-template <int HD, int P>
-__device__ __forceinline__ void dsum2(const float* t1, const float (&b1)[HD], f32x16& acc1, const float* t2,
-                                      const float (&b2)[HD], f32x16& acc2) {
-  f32x4 c1 = lds4(t1), c2 = lds4(t2);
-#pragma unroll
-  for (int k4 = 0; k4 < HD; k4 += 4) {
-    f32x4 n1 = c1, n2 = c2;
-    if (k4 + 4 < HD) {
-      n1 = lds4(t1 + k4 + 4);
-      n2 = lds4(t2 + k4 + 4);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      acc1 = mma(c1[e], b1[k4 + e], acc1);
-      acc2 = mma(c2[e], b2[k4 + e], acc2);
-    }
-    c1 = n1;
-    c2 = n2;
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
 // acc[db] += A^T x over 32 rows: A column 32 db + l32 of `t` read at the rows
 // of step r (one group of four steps ahead), x = the lane's element r.
 template <int DB, int P>
@@ -255,6 +237,33 @@ __device__ __forceinline__ void rsum16x2(const float* t1, const f32x4 (&x1)[2], 
       c1[i] = n1[i];
       c2[i] = n2[i];
     }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// acc[db] += A^T x over the 32 rows of a tile (two 16-row blocks qb): A
+// column 16 db + l16 of t at row 16 qb + 4 g + s, x = the lane's element s
+// of block qb.
+template <int DB16, int P>
+__device__ __forceinline__ void rsum16(const float* t, const f32x4 (&x)[2], f32x4 (&acc)[DB16], int l16, int g) {
+  constexpr int NG = 2 * DB16;
+  float c[4], n[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = t[(4 * g + i) * P + l16];
+#pragma unroll
+  for (int q = 0; q < NG; ++q) {
+    const int db = q >> 1, qb = q & 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) n[i] = c[i];
+    if (q + 1 < NG) {
+      const int db1 = (q + 1) >> 1, qb1 = (q + 1) & 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) n[i] = t[(16 * qb1 + 4 * g + i) * P + 16 * db1 + l16];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[db] = mma16(c[i], x[qb][i], acc[db]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = n[i];
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -435,25 +444,30 @@ void fwd_f32_kernel(FwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ: each wave owns 32 query rows (the accumulator columns) and streams
-// 32-row K/V tiles: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.
+// dQ recomputing S and dP (the backward without a dS workspace): each wave
+// owns 16 query rows (the accumulator columns of the 16 x 16 x 4 MFMA) and
+// streams 32-row K/V tiles: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.  Q,
+// dO and dQ take D/4 values per lane: two waves per SIMD at D <= 128, one
+// at D = 256.
 template <int D>
-struct F32Dq {
-  static constexpr int NW = D == 128 ? 4 : 8;
-  static constexpr int WPE = D == 128 ? 1 : 2;
-  static constexpr int BM = 32 * NW;
+struct F32Dq16 {
+  static constexpr int NW = D == 256 ? 4 : 8;
+  static constexpr int WPE = D == 256 ? 1 : 2;
+  static constexpr int BM = 16 * NW;  // query rows per workgroup
 };
 
 template <int D, bool SOFTCAP, bool ALIBI>
-__global__ __launch_bounds__(F32Dq<D>::NW * 64) __attribute__((amdgpu_waves_per_eu(F32Dq<D>::WPE, F32Dq<D>::WPE)))
-void bwd_dq_f32_kernel(BwdArgs a) {
+__global__ __launch_bounds__(F32Dq16<D>::NW * 64)
+__attribute__((amdgpu_waves_per_eu(F32Dq16<D>::WPE, F32Dq16<D>::WPE)))
+void bwd_dq16_f32_kernel(BwdArgs a) {
   using namespace f32m;
-  constexpr int NW = F32Dq<D>::NW, BM = F32Dq<D>::BM;
+  constexpr int NW = F32Dq16<D>::NW, BM = F32Dq16<D>::BM;
+  constexpr int HD4 = D / 4, DB16 = D / 16;
   using C = Cfg<D, NW>;
   __shared__ __attribute__((aligned(16))) float sK[2][C::TILE];
   __shared__ __attribute__((aligned(16))) float sV[2][C::TILE];
   const Shape& p = a.p;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, h = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g = lane >> 4;
   const int nbh = p.B * p.Hq;
   int kq, bh;
   if (!xcd_lpt_item(blockIdx.x, a.ntiles, nbh, kq, bh)) {
@@ -462,19 +476,20 @@ void bwd_dq_f32_kernel(BwdArgs a) {
   }
   const int qt = a.ntiles - 1 - kq;
   const int hq = bh % p.Hq, b = bh / p.Hq, hk = hq / p.G;
-  const int m0 = qt * BM, mw = m0 + 32 * wave, my_m = mw + l32;
+  const int m0 = qt * BM, mw = m0 + 16 * wave, my_m = mw + l16;
   const float* qp = (const float*)a.q.data + b * a.q.sb + hq * a.q.sh;
   const float* dop = (const float*)a.dout.data + b * a.dout.sb + hq * a.dout.sh;
   const float* kp = (const float*)a.k.data + b * a.k.sb + hk * a.k.sh;
   const float* vp = (const float*)a.v.data + b * a.v.sb + hk * a.v.sh;
 
-  float q[C::HD], dO[C::HD];
+  // Q and dO as the B operands of S^T = K Q^T and dP^T = V dO^T: Q[my_m][g*D/4 + s].
+  float q[HD4], dO[HD4];
   {
     const int rq = min(my_m, p.Sq - 1);
-    const float* s1 = qp + (int64_t)rq * a.q.ss + h * C::HD;
-    const float* s2 = dop + (int64_t)rq * a.dout.ss + h * C::HD;
+    const float* s1 = qp + (int64_t)rq * a.q.ss + g * HD4;
+    const float* s2 = dop + (int64_t)rq * a.dout.ss + g * HD4;
 #pragma unroll
-    for (int s = 0; s < C::HD; s += 4) {
+    for (int s = 0; s < HD4; s += 4) {
       const f32x4 x = *(const f32x4*)(s1 + s);
       const f32x4 y = *(const f32x4*)(s2 + s);
 #pragma unroll
@@ -495,7 +510,7 @@ void bwd_dq_f32_kernel(BwdArgs a) {
   int kv_lo = 0, kv_hi = p.Skv;
   if (p.causal) kv_hi = min(kv_hi, m0 + BM);
   if (p.window > 0) kv_lo = max(0, m0 - p.window);
-  const int mlast = min(mw + 31, p.Sq - 1);
+  const int mlast = min(mw + 15, p.Sq - 1);
   const bool wave_live = mw < p.Sq;
   int w_lo = kv_lo, w_hi = kv_hi;
   if (p.causal) w_hi = min(w_hi, mlast + 1);
@@ -520,11 +535,11 @@ void bwd_dq_f32_kernel(BwdArgs a) {
   const unsigned row_w = (unsigned)max(row_hi - row_lo, 0);
   const unsigned char* brow = p.blk && wave_live ? block_row(p, b, hq, mw) : nullptr;
 
-  f32x16 acc[C::DB];
+  f32x4 acc[DB16];
 #pragma unroll
-  for (int db = 0; db < C::DB; ++db)
+  for (int db = 0; db < DB16; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+    for (int r = 0; r < 4; ++r) acc[db][r] = 0.f;
 
   Tile<D, NW> sk, sv;
   const int n_first = (kv_lo / kTile) * kTile;
@@ -545,24 +560,30 @@ void bwd_dq_f32_kernel(BwdArgs a) {
     }
     const bool on = wave_live && n0 < w_hi && n0 + kTile > w_lo && (!brow || brow[n0 / kBlk] != 0);
     if (on) {
-      f32x16 s, dp;
+      f32x4 s[2], dp[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
-      const int ro = l32 * C::P + h * C::HD;
-      dsum2<C::HD, C::P>(sK[buf] + ro, q, s, sV[buf] + ro, dO, dp);
-      const int a0 = row_lo - n0 - 4 * h;
+      for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int j = n0 + blk_row(r, h);
-        float t = 0.f;
-        const float x = score<SOFTCAP, ALIBI>(s[r], p, slope, my_m, j, t);
-        const float pj = (unsigned)(8 * (r >> 2) + (r & 3) - a0) < row_w ? expf(x - lse) : 0.f;
-        float ds = pj * (dp[r] - dl) * p.scale;
-        if constexpr (SOFTCAP) ds *= (1.0f - t * t);
-        s[r] = ds;
+        for (int r = 0; r < 4; ++r) s[kb][r] = dp[kb][r] = 0.f;
+        const int ro = (16 * kb + l16) * C::P + g * HD4;
+        dsum16x2<HD4>(sK[buf] + ro, q, s[kb], sV[buf] + ro, dO, dp[kb]);
       }
-      // dQ^T += K^T dS^T: A = K[row of step r][32 db + l32], B = dS^T (element r)
-      rsum<C::DB, C::P>(sK[buf], l32, h, s, acc);
+      // element (kb, r): key n0 + 16 kb + 4 g + r of query row my_m
+      const int a0 = row_lo - n0 - 4 * g;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = n0 + 16 * kb + 4 * g + r;
+          float t = 0.f;
+          const float x = score<SOFTCAP, ALIBI>(s[kb][r], p, slope, my_m, j, t);
+          const float pj = (unsigned)(16 * kb + r - a0) < row_w ? expf(x - lse) : 0.f;
+          float ds = pj * (dp[kb][r] - dl) * p.scale;
+          if constexpr (SOFTCAP) ds *= (1.0f - t * t);
+          s[kb][r] = ds;
+        }
+      // dQ^T += K^T dS^T over the tile's 32 keys
+      rsum16<DB16, C::P>(sK[buf], s, acc, l16, g);
     }
     if (more) {
       sk.commit(tid);
@@ -574,14 +595,7 @@ void bwd_dq_f32_kernel(BwdArgs a) {
   if (my_m < p.Sq) {
     float* op = (float*)a.dq.data + b * a.dq.sb + hq * a.dq.sh + (int64_t)my_m * a.dq.ss;
 #pragma unroll
-    for (int db = 0; db < C::DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f32x4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[db][4 * i + e];
-        *(f32x4*)(op + 32 * db + 8 * i + 4 * h) = v;
-      }
+    for (int db = 0; db < DB16; ++db) *(f32x4*)(op + 16 * db + 4 * g) = acc[db];
   }
 }
 
@@ -949,15 +963,13 @@ hipError_t FLEXATT_CAT(fwd_f32_d, FLEXATT_D)(const FwdArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-#if FLEXATT_D <= 128
 hipError_t FLEXATT_CAT(bwd_dq_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
-  using F = F32Dq<FLEXATT_D>;
+  using F = F32Dq16<FLEXATT_D>;
   BwdArgs x = a;
   x.ntiles = (a.p.Sq + F::BM - 1) / F::BM;
-  FLEXATT_F32_LAUNCH(bwd_dq_f32_kernel, dim3(x.ntiles * a.p.B * a.p.Hq), dim3(F::NW * 64), st, x);
+  FLEXATT_F32_LAUNCH(bwd_dq16_f32_kernel, dim3(x.ntiles * a.p.B * a.p.Hq), dim3(F::NW * 64), st, x);
   return hipGetLastError();
 }
-#endif
 hipError_t FLEXATT_CAT(bwd_dkdv_f32_d, FLEXATT_D)(const BwdArgs& a, hipStream_t st) {
   using F = F32Kv16<FLEXATT_D>;
   BwdArgs x = a;

@@ -109,9 +109,9 @@ hipError_t bwd_kv_ds_f16_d256(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_bf16_d256(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_f16_d256(const BwdArgs&, hipStream_t);
 
-// fp32 inputs on the fp32 matrix cores (f32_mfma.hip): forward and dK/dV at
-// every D, dQ from the staged dS at every D, the recomputing dQ at D <= 128
-// (D = 256: on the vector ALUs, simt.hip).
+// fp32 inputs on the fp32 matrix cores (f32_mfma.hip): forward, dK/dV (with
+// or without writing dS), dQ from the staged dS and dQ recomputing S and dP,
+// every D.
 hipError_t fwd_f32_d32(const FwdArgs&, hipStream_t);
 hipError_t fwd_f32_d64(const FwdArgs&, hipStream_t);
 hipError_t fwd_f32_d128(const FwdArgs&, hipStream_t);
@@ -119,12 +119,11 @@ hipError_t fwd_f32_d256(const FwdArgs&, hipStream_t);
 hipError_t bwd_dq_f32_d32(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_f32_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_f32_d128(const BwdArgs&, hipStream_t);
+hipError_t bwd_dq_f32_d256(const BwdArgs&, hipStream_t);
 hipError_t bwd_dkdv_f32_d32(const BwdArgs&, hipStream_t);
 hipError_t bwd_dkdv_f32_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_dkdv_f32_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_dkdv_f32_d256(const BwdArgs&, hipStream_t);
-hipError_t bwd_dq_simt_f32_d256(const BwdArgs&, hipStream_t);
-// fp32 dK/dV writing its dS in fp32, and dQ = dS K from it.
 hipError_t bwd_kv_ds_f32_d32(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_ds_f32_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_ds_f32_d128(const BwdArgs&, hipStream_t);
