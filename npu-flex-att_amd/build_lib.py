@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libflexatt.so")
 HEAD_DIMS = (32, 64, 128, 256)
-PER_D_SOURCES = ("fwd_mfma.hip", "fwd_decode.hip", "bwd_mfma.hip", "bwd_kv.hip", "bwd_q.hip", "bwd_dq_ds.hip",
+PER_D_SOURCES = ("fwd_mfma.hip", "fwd_ws.hip", "fwd_decode.hip", "bwd_mfma.hip", "bwd_kv.hip", "bwd_q.hip", "bwd_dq_ds.hip",
                   "f32_mfma.hip")
 SINGLE_SOURCES = ("delta.hip", "capi.hip")
 

@@ -75,6 +75,10 @@ FLEXATT_DECL_D(64)
 FLEXATT_DECL_D(128)
 FLEXATT_DECL_D(256)
 #undef FLEXATT_DECL_D
+// D = 256 forward with wave-specialised pairs (fwd_ws.hip), called by the
+// D = 256 forward launcher
+hipError_t fwd_ws_bf16_d256(const FwdArgs&, hipStream_t);
+hipError_t fwd_ws_f16_d256(const FwdArgs&, hipStream_t);
 
 hipError_t bwd_delta(int dtype, const DeltaArgs&, hipStream_t);
 
