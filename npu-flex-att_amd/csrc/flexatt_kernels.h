@@ -79,6 +79,7 @@ FLEXATT_DECL_D(256)
 // D = 256 forward launcher
 hipError_t fwd_ws_bf16_d256(const FwdArgs&, hipStream_t);
 hipError_t fwd_ws_f16_d256(const FwdArgs&, hipStream_t);
+bool fwd_ws_fits(const Shape& p);  // its LDS (with a block map's lists) fits one CU
 
 hipError_t bwd_delta(int dtype, const DeltaArgs&, hipStream_t);
 

@@ -39,7 +39,10 @@
 //  * The lazy rescale, the interval masks and the mask-free interior tiles
 //    are those of fwd_mfma.hip; O leaves through a per-pair LDS tile as
 //    16-byte row-contiguous stores.
-// Block-sparse maps keep the 4-wave form of fwd_mfma.hip.
+//  * Block-sparse maps (BLK): the workgroup walks only the KV tiles whose
+//    128 x 128 block is computed for some pair (a list built in LDS at the
+//    start, as fwd_mfma.hip); in a listed tile, an S-wave whose own block is
+//    removed skips its MFMAs and hands P = 0, alpha = 1 to its partner.
 #include "flexatt_device.h"
 #include "flexatt_kernels.h"
 
@@ -73,7 +76,7 @@ struct WsCfg {
 
 constexpr float kWsRescaleThreshold = 8.0f;  // log2 units (as fwd_mfma.hip)
 
-template <class T, bool SOFTCAP, bool ALIBI>
+template <class T, bool SOFTCAP, bool ALIBI, bool BLK>
 __global__ __launch_bounds__(WsCfg::NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_ws_kernel(FwdArgs a) {
   using C = WsCfg;
@@ -119,7 +122,47 @@ void fwd_ws_kernel(FwdArgs a) {
     kv_hi = min(kv_hi, h1);
   }
   const int t_lo = kv_lo / C::BN;
-  const int nv = max((kv_hi + C::BN - 1) / C::BN - t_lo, 0);  // tiles walked
+  const int t_hi = (kv_hi + C::BN - 1) / C::BN;
+  int nv = max(t_hi - t_lo, 0);  // tiles walked
+
+  // Block-sparse maps: each pair's row of the block map over the
+  // workgroup's KV range, then the list of the tiles whose block is computed
+  // for some pair (walk position v -> tile tile_of(v)), in dynamic LDS.
+  extern __shared__ unsigned char sblk[];
+  __shared__ int s_nv;
+  const int bstride = a.bstride;
+  unsigned short* tlist = (unsigned short*)(sblk + C::NP * bstride);
+  const int kb_base = t_lo * C::BN / kBlk;
+  if (BLK && nv > 0) {
+    if (s_wave) {
+      const unsigned char* row = block_row(p, b, hq, min(mw, p.Sq - 1));
+      const int nkb = (t_hi * C::BN - 1) / kBlk - kb_base + 1;
+      for (int i = lane; i < nkb; i += 64) sblk[pr * bstride + i] = row[kb_base + i];
+    }
+    __syncthreads();
+    if (wave == 0) {
+      int base = 0;
+      for (int t0 = t_lo; t0 < t_hi; t0 += 64) {
+        const int t = t0 + lane;
+        bool live = false;
+        if (t < t_hi) {
+          const int kb = t * C::BN / kBlk - kb_base;
+#pragma unroll
+          for (int w = 0; w < C::NP; ++w) live = live || sblk[w * bstride + kb] != 0;
+        }
+        const unsigned long long m = __builtin_amdgcn_ballot_w64(live);
+        if (live) tlist[base + __builtin_popcountll(m & ((1ull << lane) - 1))] = (unsigned short)(t - t_lo);
+        base += __builtin_popcountll(m);
+      }
+      if (lane == 0) s_nv = base;
+    }
+    __syncthreads();
+    nv = __builtin_amdgcn_readfirstlane(s_nv);
+  }
+  auto tile_of = [&](int v) -> int {
+    if constexpr (BLK) return t_lo + __builtin_amdgcn_readfirstlane((int)tlist[v]);
+    else return t_lo + v;
+  };
 
   // exchange buffer of tile u: this pair's P operands and alpha
   auto xp = [&](int u) { return smem + C::XOFF + (u & 1) * (C::NP * C::XPAIR) + pr * C::XPAIR; };
@@ -182,9 +225,12 @@ void fwd_ws_kernel(FwdArgs a) {
     __syncthreads();  // prologue: K tile 0 landed
     for (int u = 0; u <= nv; ++u) {
       const bool act = u < nv;
+      const int n0 = act ? tile_of(u) * C::BN : 0;
+      // a removed block of this pair (listed for another pair): P = 0
+      const bool live = !BLK || !act || sblk[pr * bstride + n0 / kBlk - kb_base] != 0;
       f32x16 s;
       // ---- M(u): S^T of tile u --------------------------------------------
-      if (act) {
+      if (act && live) {
         const char* sK = smem + C::KOFF + (u % C::SLOTS) * C::TILEB;
         s = f32x16{};
 #pragma unroll
@@ -202,8 +248,12 @@ void fwd_ws_kernel(FwdArgs a) {
       __syncthreads();  // X(u)
       __builtin_amdgcn_sched_barrier(0);
       // ---- V(u): softmax of tile u -> exchange buffer u & 1 ----------------
-      if (act) {
-        const int n0 = (t_lo + u) * C::BN;
+      if (act && !live) {
+        char* x = xp(u);
+        *(V8*)(x + lane * 16) = V8{};
+        *(V8*)(x + 1024 + lane * 16) = V8{};
+        *(float*)(x + 2048 + lane * 4) = 1.f;
+      } else if (act) {
         if constexpr (!RAW) {
           const float fb = (float)(my_m - n0 - 4 * h);  // i - j = fb - (8 (r / 4) + r % 4)
 #pragma unroll
@@ -278,7 +328,7 @@ void fwd_ws_kernel(FwdArgs a) {
       vchk[e] = swz_tr_inv<C::CPR>(crow[e], q % C::CPR);
     }
     auto copy = [&](const T* base, int64_t ss, const int (&chk)[C::E], int ring, int v) {
-      const int n0 = (t_lo + min(v, nv - 1)) * C::BN;
+      const int n0 = tile_of(min(v, nv - 1)) * C::BN;
       const unsigned dst = lds0 + ring + (v % C::SLOTS) * C::TILEB + pr * C::E * 1024;
 #pragma unroll
       for (int e = 0; e < C::E; ++e) {
@@ -390,6 +440,14 @@ void fwd_ws_kernel(FwdArgs a) {
   }
 }
 
+// dynamic LDS of the block-sparse form: the pairs' block-map rows and the tile list
+static size_t ws_dyn_lds(const Shape& p, int bstride) {
+  return p.blk ? (size_t)WsCfg::NP * bstride + 2 * (size_t)((p.Skv + WsCfg::BN - 1) / WsCfg::BN + 2) : 0;
+}
+bool fwd_ws_fits(const Shape& p) {
+  return WsCfg::LDSB + ws_dyn_lds(p, (p.blk_nk + 3) & ~3) <= 160 * 1024;
+}
+
 template <class T>
 hipError_t launch_fwd_ws(const FwdArgs& a, hipStream_t st) {
   using C = WsCfg;
@@ -398,13 +456,21 @@ hipError_t launch_fwd_ws(const FwdArgs& a, hipStream_t st) {
   x.gpack = gp < C::NP ? gp : C::NP;
   const int bmh = 32 * (C::NP / x.gpack);
   x.nqt = (a.p.Sq + bmh - 1) / bmh;
-  x.bstride = 0;
+  x.bstride = (a.p.blk_nk + 3) & ~3;
+  const size_t dyn = ws_dyn_lds(a.p, x.bstride);
   const dim3 grid(x.nqt * (a.p.G / x.gpack) * a.p.B * a.p.Hkv), block(C::NW * 64);
   const bool sc = a.p.cap > 0.f, al = a.p.alibi != nullptr;
-  if (sc && al) hipLaunchKernelGGL((fwd_ws_kernel<T, true, true>), grid, block, 0, st, x);
-  else if (sc) hipLaunchKernelGGL((fwd_ws_kernel<T, true, false>), grid, block, 0, st, x);
-  else if (al) hipLaunchKernelGGL((fwd_ws_kernel<T, false, true>), grid, block, 0, st, x);
-  else hipLaunchKernelGGL((fwd_ws_kernel<T, false, false>), grid, block, 0, st, x);
+  if (a.p.blk) {
+    if (sc && al) hipLaunchKernelGGL((fwd_ws_kernel<T, true, true, true>), grid, block, dyn, st, x);
+    else if (sc) hipLaunchKernelGGL((fwd_ws_kernel<T, true, false, true>), grid, block, dyn, st, x);
+    else if (al) hipLaunchKernelGGL((fwd_ws_kernel<T, false, true, true>), grid, block, dyn, st, x);
+    else hipLaunchKernelGGL((fwd_ws_kernel<T, false, false, true>), grid, block, dyn, st, x);
+  } else {
+    if (sc && al) hipLaunchKernelGGL((fwd_ws_kernel<T, true, true, false>), grid, block, 0, st, x);
+    else if (sc) hipLaunchKernelGGL((fwd_ws_kernel<T, true, false, false>), grid, block, 0, st, x);
+    else if (al) hipLaunchKernelGGL((fwd_ws_kernel<T, false, true, false>), grid, block, 0, st, x);
+    else hipLaunchKernelGGL((fwd_ws_kernel<T, false, false, false>), grid, block, 0, st, x);
+  }
   return hipGetLastError();
 }
 

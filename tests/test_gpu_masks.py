@@ -55,6 +55,9 @@ CASES = {
     # (66 forward KV tiles, 132 dK/dV query tiles, 66 dQ sub-blocks)
     "bf16_d128_blocks_long": (torch.bfloat16, 128, 1, 2, 1, 4224, 4224, dict(causal=True, blocks=(8, 2, None))),
     "fp16_d64_blocks_long_shared": (torch.float16, 64, 1, 2, 2, 4160, 4200, dict(blocks=(9, 1, 3))),
+    # the D = 256 forward's wave pairs walk 32-key tiles: 82 listed tiles
+    "bf16_d256_blocks_long_cap": (torch.bfloat16, 256, 1, 2, 1, 2600, 2600, dict(causal=True, soft_cap=30.0,
+                                                                              blocks=(10, 2, None))),
 }
 
 
