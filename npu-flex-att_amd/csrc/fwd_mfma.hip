@@ -647,7 +647,7 @@ hipError_t launch_fwd_mfma(const FwdArgs& a, hipStream_t st) {
 #define FLEXATT_FWD_WS 1  // tuning override: 0 keeps D = 256 on the 4-wave form
 #endif
   // D = 256: the wave-specialised pairs of fwd_ws.hip (block maps whose
-  // lists do not fit beside its 146 KB of LDS stay here)
+  // lists do not fit beside its 145 KB of LDS stay here)
   if constexpr (D == 256 && FLEXATT_FWD_WS) {
     if (fwd_ws_fits(a.p)) return std::is_same<T, __bf16>::value ? fwd_ws_bf16_d256(a, st) : fwd_ws_f16_d256(a, st);
   }

@@ -15,27 +15,28 @@
 //    SIMD) owns 32 query rows of one head of the (batch, KV head) group
 //    (gp heads per workgroup, as in fwd_mfma.hip).
 //  * The S-wave (p) holds the Q rows (MFMA B operands) and computes
-//    S^T = K Q^T for a 32-key tile (16 MFMAs, K rows from LDS), then the
+//    S^T = K Q^T for a 64-key tile (32 MFMAs, K rows from LDS), then the
 //    softmax: mask, row max, lazy rescale, P = exp2(y - m), row sums.  It
 //    hands P (packed, as the PV B operands) and the per-row rescale factor
 //    alpha (1 unless the running max moved) to its partner through LDS.
 //  * The PV-wave (p + 4) holds O^T in registers, rescales it by alpha when
-//    some row's max moved, and runs O^T += V^T P^T (16 MFMAs, V^T from the
+//    some row's max moved, and runs O^T += V^T P^T (32 MFMAs, V^T from the
 //    LDS transpose read).  It issues every tile copy.
 //  * Step u has two phases separated by workgroup barriers:
-//      M(u): S-wave: the S^T MFMAs of tile u;  PV-wave: the copies of K
-//            tile u+3 and V tile u+2, the packed P / alpha of tile u-1 and
-//            its first transpose reads;
-//      V(u): S-wave: the softmax of tile u, into exchange buffer u & 1;
-//            PV-wave: the PV MFMAs of tile u-1, then the wait for K tile u+1
-//            and V tile u;
+//      M(u): S-wave: the S^T MFMAs of tile u;  PV-wave: the copy of V tile
+//            u, the packed P / alpha of tile u-1 and its first transpose
+//            reads;
+//      V(u): S-wave: the softmax of tile u, into the exchange buffer;
+//            PV-wave: the PV MFMAs of tile u-1, the copy of K tile u+2, then
+//            the wait for K tile u+1 and V tile u;
 //    so each SIMD alternates between the S-wave's MFMAs and the PV-wave's
 //    MFMAs beside the S-wave's VALU work.
-//  * K and V live in rings of four 16 KB slots each: the K slot of tile u-1
-//    is free once M(u-1) ends, the V slot of tile u-2 once V(u-1) ends, so
-//    the copies issued in M(u) have three steps (K) and three and a half (V)
-//    to land.  Tiles are unpadded with the per-row chunk swizzles of
-//    fwd_mfma.hip (swz_col for K, swz_tr for V).
+//  * K and V live in rings of two 32 KB slots each: the K slot of tile u is
+//    free once M(u) ends, the V slot of tile u-2 once V(u-1) ends, so each
+//    copy has about one step to land.  (The 32-key form, a tuning override,
+//    has rings of four 16 KB slots, two exchange buffers and all copies in
+//    M(u): K tile u+3, V tile u+2.)  Tiles are unpadded with the per-row
+//    chunk swizzles of fwd_mfma.hip (swz_col for K, swz_tr for V).
 //  * The lazy rescale, the interval masks and the mask-free interior tiles
 //    are those of fwd_mfma.hip; O leaves through a per-pair LDS tile as
 //    16-byte row-contiguous stores.
@@ -58,20 +59,33 @@ struct WsCfg {
   static constexpr int D = 256;
   static constexpr int NP = 4;                    // wave pairs, one per SIMD
   static constexpr int NW = 2 * NP;
-  static constexpr int BN = 32;                   // keys per tile
+#ifdef FLEXATT_WS_BN
+  static constexpr int BN = FLEXATT_WS_BN;        // tuning override (32 or 64)
+#else
+  static constexpr int BN = 64;                   // keys per tile (12-17% faster than 32)
+#endif
+  static constexpr int NB = BN / 32;              // 32-key blocks per tile
   static constexpr int KC = D / 16;               // k chunks of S^T
   static constexpr int DB = D / 32;               // 32-row blocks of O^T
   static constexpr int CPR = D / 8;               // 16-byte chunks per row
   static constexpr int ROWB = 2 * D;              // bytes per row
   static constexpr int TILEB = BN * ROWB;         // one K or V tile (16 KB)
   static constexpr int E = TILEB / (1024 * NP);   // 1 KB copies per PV-wave per tile
-  static constexpr int SLOTS = 4;                 // ring slots of K and of V
+  // ring slots of K and of V: four 16 KB slots for 32-key tiles, two 32 KB
+  // slots for 64-key tiles (copy schedules below)
+  static constexpr int SLOTS = BN == 32 ? 4 : 2;
   static constexpr int KOFF = 0, VOFF = SLOTS * TILEB;
-  static constexpr int XPAIR = 2 * 1024 + 256;    // per pair: P (two 1 KB operands), alpha (64 floats)
-  static constexpr int XOFF = 2 * SLOTS * TILEB;  // two exchange buffers
-  static constexpr int LDSB = XOFF + 2 * NP * XPAIR;
+  static constexpr int XP = 2 * NB * 1024;        // per pair: P (2 NB operands of 1 KB), then alpha (64 floats)
+  static constexpr int XPAIR = XP + 256;
+  // exchange buffers: two for 32-key tiles; one for 64-key tiles, which is
+  // enough because the barrier that starts V(u) (where P(u) is written)
+  // waits for every wave's LDS reads of P(u-1), issued in M(u)
+  static constexpr int NX = BN == 32 ? 2 : 1;
+  static constexpr int XOFF = 2 * SLOTS * TILEB;
+  static constexpr int LDSB = XOFF + NX * NP * XPAIR;
   static constexpr int RA = 4;                    // PV-wave: transpose reads this many MFMAs ahead
-  static_assert(E * 1024 * NP == TILEB && LDSB <= 160 * 1024, "LDS layout");
+  static_assert((BN == 32 || BN == 64) && E * 1024 * NP == TILEB && LDSB <= 160 * 1024, "LDS layout");
+  static_assert(SLOTS * TILEB >= NP * 32 * ROWB, "O leaves through the K ring");
 };
 
 constexpr float kWsRescaleThreshold = 8.0f;  // log2 units (as fwd_mfma.hip)
@@ -165,7 +179,7 @@ void fwd_ws_kernel(FwdArgs a) {
   };
 
   // exchange buffer of tile u: this pair's P operands and alpha
-  auto xp = [&](int u) { return smem + C::XOFF + (u & 1) * (C::NP * C::XPAIR) + pr * C::XPAIR; };
+  auto xp = [&](int u) { return smem + C::XOFF + (u % C::NX) * (C::NP * C::XPAIR) + pr * C::XPAIR; };
 
   if (s_wave) {
     // ========================= S-wave: S^T, softmax ==========================
@@ -228,52 +242,66 @@ void fwd_ws_kernel(FwdArgs a) {
       const int n0 = act ? tile_of(u) * C::BN : 0;
       // a removed block of this pair (listed for another pair): P = 0
       const bool live = !BLK || !act || sblk[pr * bstride + n0 / kBlk - kb_base] != 0;
-      f32x16 s;
+      f32x16 s[C::NB];
       // ---- M(u): S^T of tile u --------------------------------------------
       if (act && live) {
         const char* sK = smem + C::KOFF + (u % C::SLOTS) * C::TILEB;
-        s = f32x16{};
 #pragma unroll
-        for (int kc = 0; kc < C::KC; ++kc) s = M::mma(as_v8<V8>(lds_read16(sK + koff[kc])), qf[kc], s);
+        for (int bb = 0; bb < C::NB; ++bb) s[bb] = f32x16{};
+#pragma unroll
+        for (int kc = 0; kc < C::KC; ++kc)
+#pragma unroll
+          for (int bb = 0; bb < C::NB; ++bb)
+            s[bb] = M::mma(as_v8<V8>(lds_read16(sK + bb * 32 * C::ROWB + koff[kc])), qf[kc], s[bb]);
         __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-        for (int i = 0; i < C::KC - 4; ++i) {
+        for (int i = 0; i < C::NB * C::KC - 4; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-        pin(s);
+#pragma unroll
+        for (int bb = 0; bb < C::NB; ++bb) pin(s[bb]);
       }
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();  // X(u)
       __builtin_amdgcn_sched_barrier(0);
-      // ---- V(u): softmax of tile u -> exchange buffer u & 1 ----------------
+      // ---- V(u): softmax of tile u -> exchange buffer u % NX ---------------
       if (act && !live) {
         char* x = xp(u);
-        *(V8*)(x + lane * 16) = V8{};
-        *(V8*)(x + 1024 + lane * 16) = V8{};
-        *(float*)(x + 2048 + lane * 4) = 1.f;
-      } else if (act) {
-        if constexpr (!RAW) {
-          const float fb = (float)(my_m - n0 - 4 * h);  // i - j = fb - (8 (r / 4) + r % 4)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float tv;
-            s[r] = score_log2_d<SOFTCAP, ALIBI>(s[r], p, slope_log2, fb - (float)(8 * (r >> 2) + (r & 3)), tv);
-          }
+        for (int i = 0; i < 2 * C::NB; ++i) *(V8*)(x + i * 1024 + lane * 16) = V8{};
+        *(float*)(x + C::XP + lane * 4) = 1.f;
+      } else if (act) {
+        // element (bb, r) is key n0 + 32 bb + 8 (r / 4) + 4 h + r % 4
+        if constexpr (!RAW) {
+          const float fb = (float)(my_m - n0 - 4 * h);  // i - j = fb - (32 bb + 8 (r / 4) + r % 4)
+#pragma unroll
+          for (int bb = 0; bb < C::NB; ++bb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              float tv;
+              s[bb][r] = score_log2_d<SOFTCAP, ALIBI>(s[bb][r], p, slope_log2,
+                                                     fb - (float)(32 * bb + 8 * (r >> 2) + (r & 3)), tv);
+            }
         }
         const int tn = n0 / C::BN;
         if (tn < tm_lo || tn >= tm_hi) {
-          // element r is key n0 + 8 (r / 4) + 4 h + r % 4
           const int a0 = row_lo - n0 - 4 * h;
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if ((unsigned)(8 * (r >> 2) + (r & 3) - a0) >= row_w) s[r] = kNegInf;
-          pin(s);
+          for (int bb = 0; bb < C::NB; ++bb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              if ((unsigned)(32 * bb + 8 * (r >> 2) + (r & 3) - a0) >= row_w) s[bb][r] = kNegInf;
+            pin(s[bb]);
+          }
         }
-        float mp0, mp1;
-        max16_partial(s, mp0, mp1);
-        float mx = max2(mp0, mp1);
+        float mp[2 * C::NB];
+#pragma unroll
+        for (int bb = 0; bb < C::NB; ++bb) max16_partial(s[bb], mp[2 * bb], mp[2 * bb + 1]);
+        float mx;
+        if constexpr (C::NB == 1) mx = max2(mp[0], mp[1]);
+        else mx = max2(max3(mp[0], mp[1], mp[2]), mp[3]);
         if constexpr (RAW) mx *= c2;
         mx = fmaxf(mx, swap_halves(mx));
         if (mx != mx) mx = kNegInf;
@@ -286,19 +314,22 @@ void fwd_ws_kernel(FwdArgs a) {
           m_run = m_new;
         }
         const float m_use = (m_run == kNegInf) ? 0.f : m_run;
-        f32x16 e;
+        char* x = xp(u);
         float rs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          if constexpr (RAW) e[r] = fast_exp2(__builtin_fmaf(s[r], c2, -m_use));
-          else e[r] = fast_exp2(s[r] - m_use);
-          rs[r & 3] += e[r];
+        for (int bb = 0; bb < C::NB; ++bb) {
+          f32x16 e;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            if constexpr (RAW) e[r] = fast_exp2(__builtin_fmaf(s[bb][r], c2, -m_use));
+            else e[r] = fast_exp2(s[bb][r] - m_use);
+            rs[r & 3] += e[r];
+          }
+          *(V8*)(x + (2 * bb) * 1024 + lane * 16) = pack8<T>(e, 0);
+          *(V8*)(x + (2 * bb + 1) * 1024 + lane * 16) = pack8<T>(e, 8);
         }
         l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
-        char* x = xp(u);
-        *(V8*)(x + lane * 16) = pack8<T>(e, 0);
-        *(V8*)(x + 1024 + lane * 16) = pack8<T>(e, 8);
-        *(float*)(x + 2048 + lane * 4) = alpha;
+        *(float*)(x + C::XP + lane * 4) = alpha;
       }
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();  // Y(u)
@@ -307,7 +338,7 @@ void fwd_ws_kernel(FwdArgs a) {
     // 1 / l to the partner, LSE out
     const float l_tot = l_run + swap_halves(l_run);
     const bool empty = !(l_tot > 0.f);
-    *(float*)(xp(0) + 2048 + lane * 4) = empty ? 0.f : 1.0f / l_tot;
+    *(float*)(xp(0) + C::XP + lane * 4) = empty ? 0.f : 1.0f / l_tot;
     if (my_m < p.Sq && h == 0)
       a.lse[(int64_t)(b * p.Hq + hq) * p.Sq + my_m] = empty ? kNegInf : (m_run + log2f(l_tot)) * kLn2;
     __syncthreads();  // E
@@ -351,27 +382,40 @@ void fwd_ws_kernel(FwdArgs a) {
 #pragma unroll
     for (int db = 0; db < C::DB; ++db) acc[db] = f32x16{};
 
-    // Prologue: K0 V0 K1 V1 K2, then K tile u+3 and V tile u+2 in M(u).  At
-    // the end of V(u) K tile u+1 and V tile u have landed when at most the
-    // 4E loads of M(u-1) and M(u) are in flight (for u = 0, 1 those issued
-    // after K1 and after K2 in the prologue are 4E as well).
+    // Four slots: prologue K0 V0 K1 V1 K2, then K tile u+3 and V tile u+2 in
+    // M(u).  At the end of V(u) K tile u+1 and V tile u have landed when at
+    // most the 4E loads of M(u-1) and M(u) are in flight (for u = 0, 1 those
+    // issued after K1 and after K2 in the prologue are 4E as well).
+    // Two slots: prologue K0 K1, then V tile u in M(u) (into the slot of V
+    // tile u-2, read in V(u-1)) and K tile u+2 in V(u) after the MFMAs (the
+    // slot of K tile u, read in M(u)).  At the end of V(u) K tile u+1 and V
+    // tile u have landed when at most the E loads of K tile u+2 are in flight.
+    constexpr int WAITN = C::SLOTS == 4 ? 4 * C::E : C::E;
     if (nv > 0) {
       copy_k(0);
-      copy_v(0);
-      copy_k(1);
-      copy_v(1);
-      copy_k(2);
-      wait_vmcnt<4 * C::E>();  // K0 landed
+      if constexpr (C::SLOTS == 4) {
+        copy_v(0);
+        copy_k(1);
+        copy_v(1);
+        copy_k(2);
+      } else {
+        copy_k(1);
+      }
+      wait_vmcnt<WAITN>();  // K0 landed
     }
     __syncthreads();  // prologue
     for (int u = 0; u <= nv; ++u) {
       const bool act = u > 0;
       // ---- M(u): copies, P / alpha of tile u-1, first transpose reads -------
       if (nv > 0) {
-        copy_k(u + 3);
-        copy_v(u + 2);
+        if constexpr (C::SLOTS == 4) {
+          copy_k(u + 3);
+          copy_v(u + 2);
+        } else {
+          copy_v(u);
+        }
       }
-      V8 P[2];
+      V8 P[2 * C::NB];
       float alpha = 1.f;
       i16x4 blo[C::RA + 1], bhi[C::RA + 1];
       const char* sV = smem + C::VOFF + ((u + C::SLOTS - 1) % C::SLOTS) * C::TILEB;  // V tile u-1
@@ -383,9 +427,9 @@ void fwd_ws_kernel(FwdArgs a) {
       };
       if (act) {
         const char* x = xp(u - 1);
-        P[0] = *(const V8*)(x + lane * 16);
-        P[1] = *(const V8*)(x + 1024 + lane * 16);
-        alpha = *(const float*)(x + 2048 + lane * 4);
+#pragma unroll
+        for (int i = 0; i < 2 * C::NB; ++i) P[i] = *(const V8*)(x + i * 1024 + lane * 16);
+        alpha = *(const float*)(x + C::XP + lane * 4);
 #pragma unroll
         for (int j = 0; j < C::RA; ++j) rdV(j, blo[j], bhi[j]);
       }
@@ -399,22 +443,26 @@ void fwd_ws_kernel(FwdArgs a) {
           for (int db = 0; db < C::DB; ++db) scale_inplace(acc[db], alpha);
         }
 #pragma unroll
-        for (int j = 0; j < 2 * C::DB; ++j) {
+        for (int j = 0; j < 2 * C::NB * C::DB; ++j) {
           __builtin_amdgcn_sched_barrier(0);
-          if (j + C::RA < 2 * C::DB) rdV(j + C::RA, blo[(j + C::RA) % (C::RA + 1)], bhi[(j + C::RA) % (C::RA + 1)]);
+          if (j + C::RA < 2 * C::NB * C::DB)
+            rdV(j + C::RA, blo[(j + C::RA) % (C::RA + 1)], bhi[(j + C::RA) % (C::RA + 1)]);
           const V8 av = cat_tr<V8>(blo[j % (C::RA + 1)], bhi[j % (C::RA + 1)]);
           acc[j % C::DB] = M::mma(av, P[j / C::DB], acc[j % C::DB]);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (nv > 0) wait_vmcnt<4 * C::E>();  // K tile u+1, V tile u
+      if constexpr (C::SLOTS == 2) {
+        if (nv > 0) copy_k(u + 2);
+      }
+      if (nv > 0) wait_vmcnt<WAITN>();  // K tile u+1, V tile u
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();  // Y(u)
       __builtin_amdgcn_sched_barrier(0);
     }
     wait_vmcnt<0>();  // no copy may land after the workgroup's LDS is released
     __syncthreads();  // E: 1 / l is in the exchange buffer, every ring read is done
-    const float inv = *(const float*)(xp(0) + 2048 + lane * 4);
+    const float inv = *(const float*)(xp(0) + C::XP + lane * 4);
     // O through the K ring (free now): this pair's 32 x D row-major tile,
     // 16-byte chunk c of row r at c ^ (r % CPR), then row-contiguous stores.
     char* so = smem + C::KOFF + pr * 32 * C::ROWB;
