@@ -57,7 +57,7 @@ namespace flexatt {
 
 #if FLEXATT_D == 128 || FLEXATT_D == 64 || FLEXATT_D == 256
 
-template <int D>
+template <int D, int TPS = 1>
 struct KvCfg {
   static constexpr int NP = 4;                     // wave pairs, one per SIMD
   static constexpr int NW = 2 * NP;                // waves per workgroup
@@ -82,8 +82,8 @@ struct KvCfg {
   static constexpr bool PASSES = D == 256;
   static constexpr int XSLOTS = PASSES ? 2 : 4;    // 1 KB slots per pair: P, P, dS, dS (or P, P / dS, dS)
   static constexpr int XB = XSLOTS * 64 * 16;
-  static constexpr int XOFF = STAGES * STAGEB;     // two exchange buffers
-  static constexpr int LDSB = XOFF + 2 * NP * XB;
+  static constexpr int XOFF = STAGES * STAGEB;     // two exchange buffers (one of TPS tiles when TPS > 1)
+  static constexpr int LDSB = XOFF + (TPS > 1 ? TPS : 2) * NP * XB;
   static constexpr int RPW = BM / NP;              // LSE / Delta rows copied per KV-wave
   static_assert(E * 1024 * NP == TILEB, "tile must split into 1 KB copies");
   static_assert(RPW == 8, "each KV-wave copies 8 LSE and 8 Delta values");
@@ -91,11 +91,14 @@ struct KvCfg {
 };
 
 // PASS 0: dV and dK together; PASS 1: dV only; PASS 2: dK only (with the
-// staged dS when DS).
-template <class T, int D, bool SOFTCAP, bool ALIBI, bool DS, int PASS, bool BLK>
+// staged dS when DS).  TPS: tiles per step (two: both phases of a step run
+// two consecutive tiles of the walk, 32 MFMAs per wave and phase, with one
+// exchange buffer; D = 128 without block maps).
+template <class T, int D, bool SOFTCAP, bool ALIBI, bool DS, int PASS, bool BLK, int TPS = 1>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(KvCfg<D>::WPE, KvCfg<D>::WPE)))
 void bwd_kv_kernel(BwdArgs a) {
-  using C = KvCfg<D>;
+  using C = KvCfg<D, TPS>;
+  static_assert(TPS == 1 || (TPS == 2 && PASS == 0 && !BLK && D == 128), "two tiles per step: D = 128, no block maps");
   static_assert(C::DB == 2 * C::KC / 4 && (D == 64 || D == 128 || D == 256), "head dims 64, 128, 256");
   static_assert((PASS == 0) != C::PASSES && !(DS && PASS == 1), "passes: D = 256 only; dS staged by the dK pass");
   constexpr bool DOV = PASS != 2, DOK = PASS != 1;  // accumulate dV / dK
@@ -265,6 +268,143 @@ void bwd_kv_kernel(BwdArgs a) {
     int blk_next = 1;
     if (p.blk && ntile > 0) blk_next = blk_byte(0, BLK ? qt_at(0) : qt0);
 
+    if constexpr (TPS > 1) {
+      // Step u: tiles TPS u + w (w < TPS) of the walk, in stages sc + w.
+      // Both tiles' 2 NM MFMAs run as one stream with one read-ahead ring;
+      // past the end of the walk a tile's P and dS are written as zeros.
+      const int nstep = (ntile + TPS - 1) / TPS;
+      // This lane's 16 bytes of exchange slot i of tile w of the step.
+      auto xs = [&](int w, int i) { return smem + C::XOFF + pr * (TPS * C::XB) + (w * C::XSLOTS + i) * 1024 + lane * 16; };
+      __syncthreads();  // prologue: the first step's tiles landed
+      for (int u = 0; u <= nstep; ++u) {
+        f32x16 S[TPS], DP[TPS];
+        f32x4 L4[TPS][4];
+        if (u < nstep) {
+          int ra[TPS][C::KC];
+          const float* sR[TPS];
+#pragma unroll
+          for (int w = 0; w < TPS; ++w) {
+            const int st = sc + w < C::STAGES ? sc + w : sc + w - C::STAGES;
+#pragma unroll
+            for (int kc = 0; kc < C::KC; ++kc) ra[w][kc] = rowoff[kc] + st * C::STAGEB;
+            sR[w] = (const float*)(smem + st * C::STAGEB + 2 * C::TILEB);
+            f32x4 D4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) D4[i] = __builtin_bit_cast(f32x4, lds_read16(sR[w] + 16 * i + 8 + 4 * h));
+            DP[w] = f32x16{D4[0][0], D4[0][1], D4[0][2], D4[0][3], D4[1][0], D4[1][1], D4[1][2], D4[1][3],
+                           D4[2][0], D4[2][1], D4[2][2], D4[2][3], D4[3][0], D4[3][1], D4[3][2], D4[3][3]};
+            S[w] = f32x16{};
+          }
+          constexpr int NT = TPS * NM;
+#ifdef FLEXATT_KV_ILV
+          // tuning variant: the tiles' MFMAs alternate (four accumulators in flight)
+          auto wk = [&](int kk, int& w, int& k) { w = kk % TPS; k = kk / TPS; };
+#else
+          auto wk = [&](int kk, int& w, int& k) { w = kk / NM; k = kk % NM; };
+#endif
+          auto rdA = [&](int kk) {
+            int w, k;
+            wk(kk, w, k);
+            return lds_read16(smem + (ra[w][k >> 1] + (k & 1) * C::TILEB));
+          };
+          i32x4 ab[5];
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) ab[kk] = rdA(kk);
+#pragma unroll
+          for (int kk = 0; kk < NT; ++kk) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (kk + 4 < NT) ab[(kk + 4) % 5] = rdA(kk + 4);
+            int w, k;
+            wk(kk, w, k);
+            if (k == LREAD) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) L4[w][i] = __builtin_bit_cast(f32x4, lds_read16(sR[w] + 16 * i + 4 * h));
+            }
+            if (k >= LCONV) {
+#pragma unroll
+              for (int jj = 0; jj < 4; ++jj) L4[w][k - LCONV][jj] *= kLog2e;
+            }
+            if (k & 1) DP[w] = M::mma(as_v8<V8>(ab[kk % 5]), vreg[k >> 1], DP[w]);
+            else S[w] = M::mma(as_v8<V8>(ab[kk % 5]), kreg[k >> 1], S[w]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int w = 0; w < TPS; ++w) {
+            pin(S[w]);
+            pin(DP[w]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();  // X(u)
+        __builtin_amdgcn_sched_barrier(0);
+        if (u < nstep) {
+#pragma unroll
+          for (int w = 0; w < TPS; ++w) {
+            if (TPS * u + w >= ntile) {
+#pragma unroll
+              for (int i = 0; i < C::XSLOTS; ++i) *(V8*)xs(w, i) = V8{};
+              continue;
+            }
+            const int hq = hk * p.G + cg;
+            const int m0 = cqt * C::BM;
+            const float sl = ALIBI ? p.alibi[hq] * kLog2e : 0.f;
+            if (++cg == p.G) {
+              cg = 0;
+              cqt += qstep;
+            }
+            // as the one-tile form below: element r is query row
+            // m0 + 8(r/4) + 4h + r%4, KV row my_kv
+            auto form = [&](auto masked) {
+              f32x16 pe, de;
+              float y[16], tt[16];
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                tt[r] = 0.f;
+                if constexpr (RAW) {
+                  y[r] = __builtin_fmaf(S[w][r], c2, -L4[w][r >> 2][r & 3]);
+                } else {
+                  const int q = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                  y[r] = score_log2<SOFTCAP, ALIBI>(S[w][r], p, sl, q, my_kv, tt[r]) - L4[w][r >> 2][r & 3];
+                }
+              }
+              __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                float e = fast_exp2(y[r]);
+                if constexpr (decltype(masked)::value) {
+                  const int a0 = q_lo - m0 - 4 * h;
+                  e = (unsigned)(8 * (r >> 2) + (r & 3) - a0) < q_w ? e : 0.f;
+                }
+                pe[r] = e;
+              }
+              __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                float ds = -pe[r] * DP[w][r];
+                if constexpr (SOFTCAP) ds *= 1.f - tt[r] * tt[r];
+                de[r] = ds;
+              }
+              __builtin_amdgcn_sched_barrier(0);
+              *(V8*)xs(w, SLOT_P) = pack8<T>(pe, 0);
+              *(V8*)xs(w, SLOT_P + 1) = pack8<T>(pe, 8);
+              *(V8*)xs(w, SLOT_DS) = pack8<T>(de, 0);
+              *(V8*)xs(w, SLOT_DS + 1) = pack8<T>(de, 8);
+            };
+            if ((m0 + C::BM > p.Sq) || kv_tail || (p.causal && m0 < kw0 + 31) ||
+                (p.window > 0 && m0 + C::BM - 1 - kw0 > p.window) || m0 < pc_lo || m0 + C::BM > pc_hi) {
+              form(std::true_type{});
+            } else {
+              form(std::false_type{});
+            }
+          }
+          sc += TPS;
+          if (sc >= C::STAGES) sc -= C::STAGES;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();  // Y(u)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
     __syncthreads();  // prologue: tile 0 landed
     for (int u = 0; u <= ntile; ++u) {
       const bool act = u < ntile;
@@ -414,6 +554,7 @@ void bwd_kv_kernel(BwdArgs a) {
       __syncthreads();  // Y(u)
       __builtin_amdgcn_sched_barrier(0);
     }
+    }  // TPS == 1
   } else {
     // ===================== KV-wave: copies, dV / dK MFMAs ====================
     f32x16 dk[C::DB], dv[C::DB];
@@ -570,7 +711,7 @@ void bwd_kv_kernel(BwdArgs a) {
       dsp = ds_at(0, ds_qt);
     }
 
-    if (ntile > 0) {
+    if (TPS == 1 && ntile > 0) {
 #pragma unroll
       for (int t = 0; t < C::AHEAD; ++t) {
 #pragma unroll
@@ -611,6 +752,104 @@ void bwd_kv_kernel(BwdArgs a) {
       }
       dsp += step * kDsUnitB;
     };
+    if constexpr (TPS > 1) {
+      // Step u: the dV / dK MFMAs of step u-1's tiles (TPS (u-1) + w, in
+      // stages s_tr2 + w) in V(u); the copies of step u+1's tiles in M(u),
+      // into the stages of step u-2's tiles (read in V(u-1)); so each copy
+      // has one step to land.  The staged dS of step u-1's live tiles leaves
+      // after the MFMAs, and the wait at the end of V(u) lets only those
+      // stores stay in flight.
+      const int nstep = (ntile + TPS - 1) / TPS;
+      int s_cp2 = 0;  // stage of the next tile to copy
+      auto copy_tile = [&]() {
+#pragma unroll
+        for (int j = 0; j < CNT; ++j) copy_op(s_cp2, j);
+        advance();
+        s_cp2 = s_cp2 + 1 == C::STAGES ? 0 : s_cp2 + 1;
+      };
+      if (ntile > 0) {
+#pragma unroll
+        for (int w = 0; w < TPS; ++w) copy_tile();
+        wait_vmcnt<0>();
+      }
+      const int xtr2 = xtr + pr * (TPS - 1) * C::XB;  // staged-dS transpose reads: pair stride TPS XB
+      auto xs = [&](int w, int i) { return smem + C::XOFF + pr * (TPS * C::XB) + (w * C::XSLOTS + i) * 1024 + lane * 16; };
+      int s_tr2 = 0;  // stage of the first tile of step u-1
+      __syncthreads();  // prologue
+      for (int u = 0; u <= nstep; ++u) {
+        const bool act = u > 0;
+        const int na = act ? min(TPS, ntile - TPS * (u - 1)) : 0;  // tiles of step u-1 in the walk
+        if (ntile > 0) {
+#pragma unroll
+          for (int w = 0; w < TPS; ++w) copy_tile();
+        }
+        V8 PP[TPS][2], PS[TPS][2];
+        i16x4 blo[RAK + 1], bhi[RAK + 1];
+        i16x4 st4[TPS][4];
+        auto rdB2 = [&](int jj, i16x4& lo, i16x4& hi) {
+          const int w = jj / NJ;
+          int db, qc;
+          bool isk;
+          jmap(jj % NJ, db, qc, isk);
+          const int st = s_tr2 + w < C::STAGES ? s_tr2 + w : s_tr2 + w - C::STAGES;
+          const int off = (isk ? 0 : C::TILEB) + 16 * qc * C::ROWB + st * C::STAGEB;
+          lo = lds_read_tr4(smem + (voff_lo[db] + off));
+          hi = lds_read_tr4(smem + (voff_hi[db] + off));
+        };
+        if (act) {
+#pragma unroll
+          for (int w = 0; w < TPS; ++w) {
+            PP[w][0] = *(const V8*)xs(w, SLOT_P);
+            PP[w][1] = *(const V8*)xs(w, SLOT_P + 1);
+            PS[w][0] = *(const V8*)xs(w, SLOT_DS);
+            PS[w][1] = *(const V8*)xs(w, SLOT_DS + 1);
+            if constexpr (DS) {
+              const char* xb = smem + xtr2 + w * C::XSLOTS * 1024;
+#pragma unroll
+              for (int f = 0; f < 2; ++f) {
+                st4[w][2 * f] = lds_read_tr4(xb + (16 * f) * 16);
+                st4[w][2 * f + 1] = lds_read_tr4(xb + (16 * f + 8) * 16);
+              }
+            }
+          }
+#pragma unroll
+          for (int jj = 0; jj < RAK; ++jj) rdB2(jj, blo[jj], bhi[jj]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();  // X(u)
+        __builtin_amdgcn_sched_barrier(0);
+        if (act) {
+#pragma unroll
+          for (int jj = 0; jj < TPS * NJ; ++jj) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (jj + RAK < TPS * NJ) rdB2(jj + RAK, blo[(jj + RAK) % (RAK + 1)], bhi[(jj + RAK) % (RAK + 1)]);
+            const int w = jj / NJ;
+            int db, qc;
+            bool isk;
+            jmap(jj % NJ, db, qc, isk);
+            const V8 av = cat_tr<V8>(blo[jj % (RAK + 1)], bhi[jj % (RAK + 1)]);
+            if (isk) dk[db] = M::mma(av, PS[w][qc], dk[db]);
+            else dv[db] = M::mma(av, PP[w][qc], dv[db]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (DS) {
+#pragma unroll
+            for (int w = 0; w < TPS; ++w)
+              if (w < na) store_ds(st4[w]);
+          }
+          s_tr2 += TPS;
+          if (s_tr2 >= C::STAGES) s_tr2 -= C::STAGES;
+        }
+        if (ntile > 0) {  // step u+1's tiles landed; this step's 2 na dS stores may stay in flight
+          if (DS && na == 2) wait_vmcnt<4>();
+          else if (DS && na == 1) wait_vmcnt<2>();
+          else wait_vmcnt<0>();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();  // Y(u)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
     __syncthreads();  // prologue
     for (int u = 0; u <= ntile; ++u) {
       const bool act = u > 0;
@@ -692,6 +931,7 @@ void bwd_kv_kernel(BwdArgs a) {
       __syncthreads();  // Y(u)
       __builtin_amdgcn_sched_barrier(0);
     }
+    }  // TPS == 1
     wait_vmcnt<0>();  // redundant copies in flight must land before the workgroup ends
 
     // dK = scale * sum dS^T Q, dV = sum P^T dO; lane = KV row.
@@ -713,6 +953,10 @@ void bwd_kv_kernel(BwdArgs a) {
     }
   }
 }
+
+#ifndef FLEXATT_KV_TPS
+#define FLEXATT_KV_TPS 2  // tiles per step at D = 128 without block maps (tuning override; 1.7% faster than 1)
+#endif
 
 template <class T, int D, bool DS>
 hipError_t launch_kv(const BwdArgs& a, hipStream_t st) {
@@ -736,6 +980,16 @@ hipError_t launch_kv(const BwdArgs& a, hipStream_t st) {
       else if (al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, true, DSP, PS, true>), grid, block, dyn, st, x);
       else hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, false, DSP, PS, true>), grid, block, dyn, st, x);
       return hipGetLastError();
+    }
+    if constexpr (D == 128 && PS == 0 && FLEXATT_KV_TPS == 2) {
+      if (!a.p.blk) {
+        constexpr int TP = FLEXATT_KV_TPS;
+        if (sc && al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, true, DSP, PS, false, TP>), grid, block, 0, st, x);
+        else if (sc) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, false, DSP, PS, false, TP>), grid, block, 0, st, x);
+        else if (al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, true, DSP, PS, false, TP>), grid, block, 0, st, x);
+        else hipLaunchKernelGGL((bwd_kv_kernel<T, D, false, false, DSP, PS, false, TP>), grid, block, 0, st, x);
+        return hipGetLastError();
+      }
     }
     if (sc && al) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, true, DSP, PS, false>), grid, block, 0, st, x);
     else if (sc) hipLaunchKernelGGL((bwd_kv_kernel<T, D, true, false, DSP, PS, false>), grid, block, 0, st, x);
