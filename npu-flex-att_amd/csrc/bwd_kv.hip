@@ -39,6 +39,9 @@
 //    KV-wave's MFMAs beside the S-wave's VALU work.  The KV-wave issues the
 //    copies of tile u+4 in M(u): a global -> LDS copy holds its wave for
 //    tens of cycles at issue, which the MFMA phases cannot afford.
+//  * At D = 128 without block maps a step runs two consecutive tiles of the
+//    walk (TPS = 2): 32 MFMAs per wave and phase, one exchange buffer of two
+//    tiles, and the copies of the next step's two tiles in M(u).
 //  * Q and dO are read two ways from the same tile, as rows (S, dP) and as
 //    columns (dV^T, dK^T, with the LDS transpose read); the dual-use swizzle
 //    keeps both conflict-free.
@@ -296,12 +299,8 @@ void bwd_kv_kernel(BwdArgs a) {
             S[w] = f32x16{};
           }
           constexpr int NT = TPS * NM;
-#ifdef FLEXATT_KV_ILV
-          // tuning variant: the tiles' MFMAs alternate (four accumulators in flight)
-          auto wk = [&](int kk, int& w, int& k) { w = kk % TPS; k = kk / TPS; };
-#else
+          // MFMA kk: tile kk / NM, its MFMA kk % NM (alternating the tiles' MFMAs measured slower)
           auto wk = [&](int kk, int& w, int& k) { w = kk / NM; k = kk % NM; };
-#endif
           auto rdA = [&](int kk) {
             int w, k;
             wk(kk, w, k);
