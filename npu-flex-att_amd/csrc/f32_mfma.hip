@@ -293,7 +293,10 @@ struct F32Fwd {
   static constexpr int BM = 32 * NW;  // query rows per workgroup
 };
 
-template <int D, bool SOFTCAP, bool ALIBI>
+// BLK: with a block map, the workgroup walks only the 32-key tiles whose
+// 128 x 128 block is computed for some of its rows (a list built in dynamic
+// LDS at the start); a wave whose own block is removed skips the tile.
+template <int D, bool SOFTCAP, bool ALIBI, bool BLK = false>
 __global__ __launch_bounds__(F32Fwd<D>::NW * 64) __attribute__((amdgpu_waves_per_eu(F32Fwd<D>::WPE, F32Fwd<D>::WPE)))
 void fwd_f32_kernel(FwdArgs a) {
   using namespace f32m;
@@ -368,27 +371,56 @@ void fwd_f32_kernel(FwdArgs a) {
 
   Tile<D, NW> st;
   const int n_first = (kv_lo / kTile) * kTile;
-  if (n_first < kv_hi) {
-    st.fetch(sK[0], kp, a.k.ss, n_first, p.Skv, tid);
+  int nv = max((kv_hi - n_first + kTile - 1) / kTile, 0);  // tiles walked
+  extern __shared__ unsigned short tlist[];  // BLK: walk position -> tile offset from n_first
+  __shared__ int s_nv;
+  if (BLK && nv > 0) {
+    if (wave == 0) {
+      const int rb0 = m0 / kBlk, rb1 = (min(m0 + BM, p.Sq) - 1) / kBlk;  // the workgroup's block rows
+      int base = 0;
+      for (int i0 = 0; i0 < nv; i0 += 64) {
+        const int i = i0 + lane;
+        bool live = false;
+        if (i < nv) {
+          const int kb = (n_first + kTile * i) / kBlk;
+          for (int rb = rb0; rb <= rb1 && !live; ++rb) live = block_row(p, b, hq, rb * kBlk)[kb] != 0;
+        }
+        const unsigned long long msk = __builtin_amdgcn_ballot_w64(live);
+        if (live) tlist[base + __builtin_popcountll(msk & ((1ull << lane) - 1))] = (unsigned short)i;
+        base += __builtin_popcountll(msk);
+      }
+      if (lane == 0) s_nv = base;
+    }
+    __syncthreads();
+    nv = __builtin_amdgcn_readfirstlane(s_nv);
+  }
+  auto tile_n0 = [&](int v) -> int {
+    if constexpr (BLK) return n_first + kTile * __builtin_amdgcn_readfirstlane((int)tlist[v]);
+    else return n_first + kTile * v;
+  };
+  if (nv > 0) {
+    st.fetch(sK[0], kp, a.k.ss, tile_n0(0), p.Skv, tid);
     st.commit(tid);
-    st.fetch(sV[0], vp, a.v.ss, n_first, p.Skv, tid);
+    st.fetch(sV[0], vp, a.v.ss, tile_n0(0), p.Skv, tid);
     st.commit(tid);
   }
   st.settle();
   __syncthreads();
   int buf = 0;
-  for (int n0 = n_first; n0 < kv_hi; n0 += kTile, buf ^= 1) {
-    const bool more = n0 + kTile < kv_hi;
+  for (int v = 0; v < nv; ++v, buf ^= 1) {
+    const int n0 = tile_n0(v);
+    const bool more = v + 1 < nv;
+    const int n1 = more ? tile_n0(v + 1) : 0;
     const bool on = wave_live && n0 < w_hi && n0 + kTile > w_lo && (!brow || brow[n0 / kBlk] != 0);
     // next K tile in flight during this tile's S^T, next V tile during its P V
-    if (more) st.fetch(sK[buf ^ 1], kp, a.k.ss, n0 + kTile, p.Skv, tid);
+    if (more) st.fetch(sK[buf ^ 1], kp, a.k.ss, n1, p.Skv, tid);
     f32x16 s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.f;
     if (on) dsum<C::HD, C::P>(sK[buf] + l32 * C::P + h * C::HD, q, s);
     if (more) {
       st.commit(tid);
-      st.fetch(sV[buf ^ 1], vp, a.v.ss, n0 + kTile, p.Skv, tid);
+      st.fetch(sV[buf ^ 1], vp, a.v.ss, n1, p.Skv, tid);
     }
     if (on) {
       // scores, mask, online softmax over this lane's 16 keys and the other half's
@@ -959,7 +991,19 @@ hipError_t FLEXATT_CAT(fwd_f32_d, FLEXATT_D)(const FwdArgs& a, hipStream_t st) {
   using F = F32Fwd<FLEXATT_D>;
   FwdArgs x = a;
   x.nqt = (a.p.Sq + F::BM - 1) / F::BM;
-  FLEXATT_F32_LAUNCH(fwd_f32_kernel, dim3(x.nqt * a.p.B * a.p.Hq), dim3(F::NW * 64), st, x);
+  const dim3 grid(x.nqt * a.p.B * a.p.Hq), block(F::NW * 64);
+  // block maps: the walk list of live 32-key tiles in dynamic LDS (up to
+  // 16 KB beside the tiles; longer key ranges walk every tile)
+  const size_t dyn = 2 * (size_t)((a.p.Skv + f32m::kTile - 1) / f32m::kTile + 2);
+  if (a.p.blk && dyn <= 16384) {
+    const bool sc = a.p.cap > 0.f, al = a.p.alibi != nullptr;
+    if (sc && al) hipLaunchKernelGGL((fwd_f32_kernel<FLEXATT_D, true, true, true>), grid, block, dyn, st, x);
+    else if (sc) hipLaunchKernelGGL((fwd_f32_kernel<FLEXATT_D, true, false, true>), grid, block, dyn, st, x);
+    else if (al) hipLaunchKernelGGL((fwd_f32_kernel<FLEXATT_D, false, true, true>), grid, block, dyn, st, x);
+    else hipLaunchKernelGGL((fwd_f32_kernel<FLEXATT_D, false, false, true>), grid, block, dyn, st, x);
+    return hipGetLastError();
+  }
+  FLEXATT_F32_LAUNCH(fwd_f32_kernel, grid, block, st, x);
   return hipGetLastError();
 }
 

@@ -58,6 +58,8 @@ CASES = {
     # the D = 256 forward's wave pairs walk 32-key tiles: 82 listed tiles
     "bf16_d256_blocks_long_cap": (torch.bfloat16, 256, 1, 2, 1, 2600, 2600, dict(causal=True, soft_cap=30.0,
                                                                               blocks=(10, 2, None))),
+    # the fp32 forward's list of 32-key tiles: 72 tiles
+    "fp32_d64_blocks_long": (torch.float32, 64, 1, 2, 1, 2200, 2300, dict(causal=True, blocks=(11, 2, None))),
 }
 
 
