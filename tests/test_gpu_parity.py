@@ -101,6 +101,24 @@ def test_fp32_several_tiles(gpu_device, d, flags):
         check(name, x, r, torch.float32)
 
 
+@pytest.mark.parametrize("case", ["bf16_g8_causal_window", "fp16_g3_alibi_noncausal"])
+def test_d256_head_groups(gpu_device, case):
+    # The D = 256 forward's wave pairs pack gp = min(G & -G, 4) heads per
+    # workgroup: G = 8 gives four heads of 32 rows each and two workgroups
+    # per group, G = 3 one head of 128 rows and three; Sq != Skv, lengths off
+    # the tile grid, several work items per head; the two-pass backward too.
+    dtype, hq, hkv, sq, skv, kw = {
+        "bf16_g8_causal_window": (torch.bfloat16, 8, 1, 150, 333, dict(causal=True, sliding_window=70)),
+        "fp16_g3_alibi_noncausal": (torch.float16, 6, 2, 300, 217, dict(causal=False, alibi=True, scale=0.05)),
+    }[case]
+    cpu, dev = draw(29, 2, hq, hkv, sq, skv, 256, dtype)
+    slopes = alibi_slopes(hq) if kw.pop("alibi", False) else None
+    got = fwd_bwd(nfa, *dev, alibi_slope=slopes.to(gpu_device) if slopes is not None else None, **kw)
+    ref = oracle_fwd_bwd(*cpu, alibi_slope=slopes, **kw)
+    for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
+        check(name, x, r, dtype)
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "fp16", "fp32"])
 def test_relative_position_score_mod(gpu_device, dtype):
     # FlexAttention's relative-position score_mod, score + (q_idx - kv_idx),
