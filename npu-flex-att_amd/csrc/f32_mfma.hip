@@ -831,9 +831,11 @@ void bwd_dkdv16_f32_kernel(BwdArgs a) {
       rsum16x2<DB16, C::P>(sO[buf], s, dv, sQ[buf], dp, dk, l16, g);
     }
     if constexpr (DS) {
+      // units of removed blocks are neither written nor read (their dS is zero)
       const int t = m0 / kDsQT;
       const int kb_lo = ds_kb_lo(t, p.window, nkb);
-      if (kb_w < nkb && kb_w >= kb_lo && kb_w < ds_kb_hi(t, p.causal, nkb)) {
+      if (kb_w < nkb && kb_w >= kb_lo && kb_w < ds_kb_hi(t, p.causal, nkb) &&
+          (!p.blk || block_row(p, b, hq, min(m0, p.Sq - 1))[kb_w] != 0)) {
         const int64_t unit = (int64_t)(b * p.Hq + hq) * a.ds_head + ds_tile_offset(t, p.causal, p.window, nkb) +
                              (kb_w - kb_lo);
         // element (query row i, KV column j) of the unit at ((j / 32) * 32 + i) * 32 + j % 32
@@ -904,6 +906,9 @@ void bwd_dq_ds_f32_kernel(BwdArgs a) {
   // unit of block kb for this wave: ubase + kb
   const int64_t ubase = (int64_t)(b * p.Hq + hq) * a.ds_head + ds_tile_offset(t, p.causal, p.window, nkb) - w_kb_lo;
   const float* dsb = (const float*)a.ds + l32 * kTile + 4 * h;
+  // block maps: the units of this wave's removed blocks are not read (never written, their dS is zero)
+  const unsigned char* brow = p.blk && wave_live ? block_row(p, b, hq, mw) : nullptr;
+  auto unit_live = [&](int kb) { return kb >= w_kb_lo && kb < w_kb_hi && (!brow || brow[kb] != 0); };
 
   f32x16 acc[C::DB];
 #pragma unroll
@@ -914,7 +919,7 @@ void bwd_dq_ds_f32_kernel(BwdArgs a) {
   // dS^T operand of one 32-row K tile: element r = dS[my_m][n0 + row of step r]
   auto load_ds = [&](int n0, f32x16& x) {
     const int kb = n0 / kDsKB;
-    if (kb >= w_kb_lo && kb < w_kb_hi) {
+    if (unit_live(kb)) {
       const float* src = dsb + (ubase + kb) * (kDsUnitB32 / 4) + ((n0 % kDsKB) / kTile) * (kTile * kTile);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -943,8 +948,7 @@ void bwd_dq_ds_f32_kernel(BwdArgs a) {
       st.fetch(sK[buf ^ 1], kp, a.k.ss, n0 + kTile, p.Skv, tid);
       load_ds(n0 + kTile, nxt);
     }
-    const int kb = n0 / kDsKB;
-    if (kb >= w_kb_lo && kb < w_kb_hi) rsum<C::DB, C::P>(sK[buf], l32, h, cur, acc);
+    if (unit_live(n0 / kDsKB)) rsum<C::DB, C::P>(sK[buf], l32, h, cur, acc);
     if (more) st.commit(tid);
     st.settle();
     __syncthreads();
