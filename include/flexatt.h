@@ -188,7 +188,7 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
  * row, KV row) pair of each query head, in 32 x 128 units over the causal /
  * window band (interval and block masks keep that band; masked pairs hold
  * zeros, and the units of removed 128 x 128 blocks are neither written nor
- * read by the fp16/bf16 kernels), followed by FLEXATT_BWD_QUEUE_BYTES of
+ * read), followed by FLEXATT_BWD_QUEUE_BYTES of
  * work-queue counters:
  * flexatt_bwd_workspace(p) bytes in all (0: the problem is outside this
  * range), 16-byte aligned, not zeroed, reusable once the call's work on
@@ -203,8 +203,25 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
  * (which the Delta pass clears), so that faster XCDs take more work (fp16/
  * bf16); with a workspace of only the dS band's size the static order is
  * kept.  Outside
- * the range it runs flexatt_bwd and the workspace may be NULL. */
+ * the range it runs flexatt_bwd and the workspace may be NULL.
+ *
+ * Bounded memory.  The band grows as Sq * Skv (about 1 byte per (query row,
+ * KV row) pair of each query head for causal fp16/bf16, 1.1 GB at B=2 Hq=32
+ * S=4096), while the reference's backward needs O(S) memory
+ * (npu_flash_attention.py:675-685).  flexatt_bwd_ws therefore also accepts:
+ *  - a workspace smaller than the whole band but holding the band of at
+ *    least one (batch, KV head) group (G = heads_q / heads_kv query heads):
+ *    the staged backward then runs in passes over chunks of whole groups
+ *    (whole batches when one fits, else KV heads of one batch), reusing the
+ *    workspace pass after pass on `stream`; smaller: FLEXATT_EINVAL;
+ *  - workspace == NULL with workspace_bytes == 0: the recomputing backward
+ *    (flexatt_bwd), O(S) memory.
+ * flexatt_bwd_workspace_limited(p, limit) is the size to allocate under a
+ * byte budget: the whole band (plus the queue counters) when it fits, else
+ * the most whole groups that fit, else 0 (no staging: pass NULL, 0).  Passes
+ * give the same results as one pass up to fp32 summation order. */
 size_t flexatt_bwd_workspace(const flexatt_problem* p);
+size_t flexatt_bwd_workspace_limited(const flexatt_problem* p, size_t limit_bytes);
 int flexatt_bwd_ws(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
                    const flexatt_tensor* v, const flexatt_tensor* o, const flexatt_tensor* dout,
                    const float* lse, float* delta, const flexatt_tensor* dq, const flexatt_tensor* dk,
@@ -230,7 +247,7 @@ const char* flexatt_status_string(int status);
 /* ABI version of this header (bumped on any signature change). */
 int flexatt_abi_version(void);
 
-#define FLEXATT_ABI_VERSION 6
+#define FLEXATT_ABI_VERSION 7
 
 #ifdef __cplusplus
 }

@@ -3,6 +3,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "../../include/flexatt.h"
@@ -255,16 +256,19 @@ BwdLauncher pick_dkdv(const flexatt_problem* p) { return kDkdv[p->dtype][head_in
     if (rc_ != FLEXATT_OK) return rc_; \
   } while (0)
 
-// CUs of the current device (cached per device), 0 if unknown.
+// CUs of the current device (cached per device), 0 if unknown.  Host threads
+// may call the ABI concurrently: the cache is atomic (a racing first lookup
+// stores the same value twice).
 int cu_count() {
-  static int cache[64];
+  static std::atomic<int> cache[kMaxDevices];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cache[dev] = n;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 int bwd_common(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
@@ -340,6 +344,50 @@ int ds_workspace(const flexatt_problem* p, void* ws, size_t bytes, BwdArgs& a) {
   a.ds = (char*)ws;
   a.ds_head = ds_units_per_head(p);
   return FLEXATT_OK;
+}
+
+// Bounded workspaces: the staged backward of a problem whose whole dS band
+// exceeds the caller's workspace runs in passes over chunks of (batch, KV
+// head) groups, each pass a problem of its own over the same buffers.  A
+// group (one KV head and its G query heads) is the smallest chunk: its dK /
+// dV sum and its dQ rows need only its own dS units.
+int64_t ds_group_bytes(const flexatt_problem* p) {
+  return (int64_t)(p->heads_q / p->heads_kv) * ds_units_per_head(p) * ds_unit_bytes(p);
+}
+// Groups per pass for a workspace of `bytes` (>= one group's band): whole
+// batches when at least one batch fits, else KV heads of one batch.
+int64_t chunk_groups(const flexatt_problem* p, size_t bytes) {
+  int64_t k = (int64_t)(bytes / (size_t)ds_group_bytes(p));
+  if (k >= p->heads_kv) k = k / p->heads_kv * p->heads_kv;
+  return k;
+}
+// One pass: batches [b0, b0 + nb) with every KV head, or (nb = 1) the KV
+// heads [h0, h0 + nh) of batch b0.
+struct Chunk {
+  int b0, nb, h0, nh;
+};
+flexatt_problem sub_problem(const flexatt_problem* p, const Chunk& c) {
+  flexatt_problem s = *p;
+  const int G = p->heads_q / p->heads_kv;
+  s.batch = c.nb;
+  s.heads_kv = c.nh;
+  s.heads_q = c.nh * G;
+  if (p->alibi_slopes) s.alibi_slopes = p->alibi_slopes + (int64_t)c.h0 * G;
+  if (p->doc_bounds) s.doc_bounds = p->doc_bounds + (int64_t)c.b0 * p->seqlen_q * 2;
+  if (p->col_bounds) s.col_bounds = p->col_bounds + (int64_t)c.b0 * p->seqlen_kv * 2;
+  if (p->block_map) {
+    const int64_t nq = (p->seqlen_q + kBlk - 1) / kBlk, nk = (p->seqlen_kv + kBlk - 1) / kBlk;
+    const bool per_head = p->block_heads == p->heads_q && p->heads_q > 1;
+    s.block_map = p->block_map + ((int64_t)c.b0 * p->block_heads + (per_head ? (int64_t)c.h0 * G : 0)) * nq * nk;
+    s.block_heads = per_head ? s.heads_q : 1;
+  }
+  return s;
+}
+// The chunk's view of a [B, H, S, D] tensor whose head h0 is at `h0`.
+flexatt_tensor sub_tensor(const flexatt_tensor* t, int dt, int64_t b0, int64_t h0) {
+  flexatt_tensor s = *t;
+  s.data = (char*)t->data + (b0 * t->stride_b + h0 * t->stride_h) * (int64_t)elt_size(dt);
+  return s;
 }
 
 }  // namespace
@@ -509,6 +557,14 @@ size_t flexatt_bwd_workspace(const flexatt_problem* p) {
   return n ? n + FLEXATT_BWD_QUEUE_BYTES : 0;
 }
 
+size_t flexatt_bwd_workspace_limited(const flexatt_problem* p, size_t limit_bytes) {
+  const size_t full = flexatt_bwd_workspace(p);
+  if (full == 0 || full <= limit_bytes) return full;
+  const size_t gb = (size_t)ds_group_bytes(p);
+  if (limit_bytes < gb + FLEXATT_BWD_QUEUE_BYTES) return 0;  // not even one group: recompute
+  return (size_t)chunk_groups(p, limit_bytes - FLEXATT_BWD_QUEUE_BYTES) * gb + FLEXATT_BWD_QUEUE_BYTES;
+}
+
 namespace {
 int run_dkdv_ds(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k, const flexatt_tensor* v,
                 const flexatt_tensor* dout, const float* lse, const float* delta, const flexatt_tensor* dk,
@@ -555,19 +611,12 @@ int flexatt_bwd_dq_ds(const flexatt_problem* p, const flexatt_tensor* k, const v
   return run_dq_ds(p, k, workspace, workspace_bytes, dq, nullptr, stream);
 }
 
-int flexatt_bwd_ws(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
-                   const flexatt_tensor* v, const flexatt_tensor* o, const flexatt_tensor* dout, const float* lse,
-                   float* delta, const flexatt_tensor* dq, const flexatt_tensor* dk, const flexatt_tensor* dv,
-                   void* workspace, size_t workspace_bytes, void* stream) {
-  FLEXATT_TRY(check_problem(p));
-  if (!ds_applies(p)) return flexatt_bwd(p, q, k, v, o, dout, lse, delta, dq, dk, dv, stream);
-  BwdArgs a;
-  FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
-  FLEXATT_TRY(check_tensor(o, p->dtype));
-  FLEXATT_TRY(check_out_tensor(dq, p->dtype, p->batch, p->heads_q, p->seqlen_q, p->head_dim));
-  FLEXATT_TRY(check_out_tensor(dk, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
-  FLEXATT_TRY(check_out_tensor(dv, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
-  FLEXATT_TRY(ds_workspace(p, workspace, workspace_bytes, a));
+namespace {
+// One staged pass (the arguments are checked): Delta, dK/dV writing dS, dQ.
+int run_staged(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k, const flexatt_tensor* v,
+               const flexatt_tensor* o, const flexatt_tensor* dout, const float* lse, float* delta,
+               const flexatt_tensor* dq, const flexatt_tensor* dk, const flexatt_tensor* dv, void* workspace,
+               size_t workspace_bytes, void* stream) {
   // queue counters after the dS band: [0], [1] the dK/dV launches, [2] dQ
   int* queue = nullptr;
   if (workspace_bytes >= ds_bytes(p) + FLEXATT_BWD_QUEUE_BYTES && (cu_count() & ~7) > 0)
@@ -575,6 +624,47 @@ int flexatt_bwd_ws(const flexatt_problem* p, const flexatt_tensor* q, const flex
   FLEXATT_TRY(run_delta(p, o, dout, delta, queue, stream));
   FLEXATT_TRY(run_dkdv_ds(p, q, k, v, dout, lse, delta, dk, dv, workspace, workspace_bytes, queue, stream));
   return run_dq_ds(p, k, workspace, workspace_bytes, dq, queue ? queue + 2 : nullptr, stream);
+}
+}  // namespace
+
+int flexatt_bwd_ws(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
+                   const flexatt_tensor* v, const flexatt_tensor* o, const flexatt_tensor* dout, const float* lse,
+                   float* delta, const flexatt_tensor* dq, const flexatt_tensor* dk, const flexatt_tensor* dv,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  FLEXATT_TRY(check_problem(p));
+  // outside the range, or no workspace at all: the recomputing backward
+  if (!ds_applies(p) || (!workspace && workspace_bytes == 0))
+    return flexatt_bwd(p, q, k, v, o, dout, lse, delta, dq, dk, dv, stream);
+  BwdArgs a;
+  FLEXATT_TRY(bwd_common(p, q, k, v, dout, lse, delta, a));
+  FLEXATT_TRY(check_tensor(o, p->dtype));
+  FLEXATT_TRY(check_out_tensor(dq, p->dtype, p->batch, p->heads_q, p->seqlen_q, p->head_dim));
+  FLEXATT_TRY(check_out_tensor(dk, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
+  FLEXATT_TRY(check_out_tensor(dv, p->dtype, p->batch, p->heads_kv, p->seqlen_kv, p->head_dim));
+  if (!workspace) return FLEXATT_EINVAL;
+  if (((uintptr_t)workspace) % 16 != 0) return FLEXATT_ELAYOUT;
+  if (workspace_bytes >= ds_bytes(p))
+    return run_staged(p, q, k, v, o, dout, lse, delta, dq, dk, dv, workspace, workspace_bytes, stream);
+  // A smaller workspace: passes over chunks of whole (batch, KV head) groups.
+  if (workspace_bytes < (size_t)ds_group_bytes(p)) return FLEXATT_EINVAL;
+  const int64_t kg = chunk_groups(p, workspace_bytes);
+  const int G = p->heads_q / p->heads_kv;
+  const int nbc = kg >= p->heads_kv ? (int)(kg / p->heads_kv) : 1;  // batches per pass
+  const int nhc = kg >= p->heads_kv ? p->heads_kv : (int)kg;        // KV heads per pass
+  for (int b0 = 0; b0 < p->batch; b0 += nbc)
+    for (int h0 = 0; h0 < p->heads_kv; h0 += nhc) {
+      const Chunk c{b0, nbc < p->batch - b0 ? nbc : p->batch - b0, h0, nhc < p->heads_kv - h0 ? nhc : p->heads_kv - h0};
+      const flexatt_problem sp = sub_problem(p, c);
+      const int64_t hq0 = (int64_t)h0 * G;
+      const flexatt_tensor sq = sub_tensor(q, p->dtype, b0, hq0), sk = sub_tensor(k, p->dtype, b0, h0),
+                           sv = sub_tensor(v, p->dtype, b0, h0), so = sub_tensor(o, p->dtype, b0, hq0),
+                           sdo = sub_tensor(dout, p->dtype, b0, hq0), sdq = sub_tensor(dq, p->dtype, b0, hq0),
+                           sdk = sub_tensor(dk, p->dtype, b0, h0), sdv = sub_tensor(dv, p->dtype, b0, h0);
+      const int64_t r0 = ((int64_t)b0 * p->heads_q + hq0) * p->seqlen_q;  // first LSE / Delta row
+      FLEXATT_TRY(run_staged(&sp, &sq, &sk, &sv, &so, &sdo, lse + r0, delta + r0, &sdq, &sdk, &sdv, workspace,
+                             workspace_bytes, stream));
+    }
+  return FLEXATT_OK;
 }
 
 }  // extern "C"

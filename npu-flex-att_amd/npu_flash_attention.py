@@ -59,9 +59,17 @@ _DTYPES = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _li
 # Set to False to force the regular forward kernel (tests compare the two).
 decode_enabled = True
 # The backward stages dS through a workspace (flexatt_bwd_ws) whenever the
-# library supports it for the problem (fp16/bf16, head_dim 128).  Set to
-# False to run the recomputing dQ kernel (flexatt_bwd).
+# library supports it for the problem (fp16/bf16 at head_dim 64, 128 and 256;
+# fp32 at every head_dim).  Set to False to run the recomputing dQ kernel
+# (flexatt_bwd).
 ds_staging_enabled = True
+# Byte budget of that workspace for one backward call.  The whole dS band
+# (about one byte per attended (query row, key) pair of each query head for
+# fp16/bf16, two for fp32) is used when it fits; otherwise the staged backward
+# runs in passes over chunks of whole (batch, KV-head) groups whose band fits,
+# and when not even one group fits the recomputing backward runs, whose memory
+# is O(S) like the reference's (npu_flash_attention.py:675-685).
+ds_workspace_limit = 4 << 30
 _HEAD_DIMS = (32, 64, 128, 256)
 _BLOCK = 128  # block edge of the block-sparse map (flexatt_problem.block_map)
 
@@ -397,6 +405,17 @@ def npu_flash_attention_backward(
     return DQ, DK, DV
 
 
+def _staged_workspace_bytes(lib, p) -> int:
+    """Workspace bytes of the staged backward for problem ``p`` under
+    ``ds_workspace_limit`` (the whole band, or the band of the chunk of whole
+    (batch, KV-head) groups one pass covers); 0 selects the recomputing
+    backward (staging disabled, outside its range, or not even one group's
+    band within the limit)."""
+    if not ds_staging_enabled:
+        return 0
+    return int(lib.flexatt_bwd_workspace_limited(p, max(0, int(ds_workspace_limit))))
+
+
 def _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, *, causal, sliding_window,
                    alibi, scale, soft_cap, masks=None):
     """Run Delta, dQ and dK/dV into the caller's ``DQ`` (kernel-ready layout)
@@ -414,11 +433,11 @@ def _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, *, causal,
     lse = lse.to(torch.float32).contiguous()
     slopes = _alibi(alibi, Hq, query.device)
     p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes, masks)
-    # head_dim 128 fp16/bf16: the dK/dV kernel stages its dS in a workspace
-    # from torch's caching allocator and dQ is formed from it
-    ws_bytes = lib.flexatt_bwd_workspace(p) if ds_staging_enabled else 0
+    ws_bytes = _staged_workspace_bytes(lib, p)
     with torch.cuda.device(query.device):
         if ws_bytes:
+            # the dK/dV kernel stages its dS in a workspace from torch's
+            # caching allocator and dQ is formed from it
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
             st = lib.flexatt_bwd_ws(p, _lib.tensor(q), _lib.tensor(k), _lib.tensor(v), _lib.tensor(o),
                                     _lib.tensor(do), lse.data_ptr(), delta.data_ptr(), _lib.tensor(DQ),

@@ -27,6 +27,22 @@ TOL = {
     torch.bfloat16: {"o": 2e-2, "lse": 5e-3, "dq": 2e-2, "dk": 2e-2, "dv": 2e-2},
 }
 
+# The fp32 bounds hold while the largest attended score (after scale,
+# soft-cap and ALiBi bias) stays within about 100: an fp32 score x carries a
+# rounding error of up to half an ulp, |x| 2^-24, which exp(x - m) passes on
+# to P, O and the gradients.  Above that the fp32 bound scales with the score
+# magnitude: tolerance x fp32_score_factor(...) = max(1, max|x| / 100).
+FP32_SCORE_REF = 100.0
+
+
+def fp32_score_factor(q, k, scale=None, soft_cap=0.0, alibi_slope=None, causal=False, sliding_window=0):
+    """max(1, max |attended score| / 100) for the fp32 tolerances."""
+    qf, kf, _, sc, _ = orc._prep(q, k, k, scale, torch.float64)
+    x, _ = orc.scores(qf, kf, sc, soft_cap, alibi_slope)
+    ok = orc.allowed_mask(x.shape[-2], x.shape[-1], causal, sliding_window)
+    return max(1.0, x.abs().masked_fill(~ok, 0.0).max().item() / FP32_SCORE_REF)
+
+
 # One dict per checked output: test id, output name, dtype, err, max-abs, tol.
 RECORDS = []
 

@@ -187,3 +187,22 @@ def test_block_map_rejections():
                        1, 1, 256, 256, "cpu")
     with pytest.raises(RuntimeError):
         nfa._block_map("not a mask", 1, 1, 256, 256, "cpu")
+
+
+def test_bench_metric_names():
+    """bench.py labels the north-star workload with BASELINE.json's metric and
+    every other workload with its own dtype and primitives."""
+    import json
+    import os
+
+    import bench
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    want = json.load(open(os.path.join(root, "BASELINE.json")))["metric"]
+    B, Hq, Hkv, Sq, Skv, D, dts, causal, window, cap, alibi, scale, _ = bench.CONFIGS["gqa_llama3_8b"]
+    assert bench.metric_name(dts, Hq, Hkv, Sq, Skv, D, causal, window, cap, alibi, scale) == want
+    names = {bench.metric_name(*c[6:7], *c[1:6], *c[7:12]) for c in bench.CONFIGS.values()}
+    assert len(names) == len(bench.CONFIGS)
+    B, Hq, Hkv, Sq, Skv, D, dts, causal, window, cap, alibi, scale, _ = bench.CONFIGS["all_primitives_d64"]
+    m = bench.metric_name(dts, Hq, Hkv, Sq, Skv, D, causal, window, cap, alibi, scale)
+    assert m.startswith("fwd+bwd attention TFLOPS & % MFMA peak, fp16 ") and "D=64" in m and "ALiBi" in m

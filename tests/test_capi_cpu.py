@@ -347,6 +347,75 @@ def test_staged_bwd_rejections():
     assert lib.flexatt_bwd_dq_ds(problem(head_dim=32), tens(), FAKE, need, tens(), None) == -6
     assert lib.flexatt_bwd_dkdv_ds(problem(head_dim=32), tens(), tens(), tens(), tens(), FAKE, FAKE, tens(),
                                    tens(), FAKE, need, None) == -6
-    assert lib.flexatt_bwd_ws(p, t, t, t, t, t, FAKE, FAKE, t, t, t, FAKE, band - 1, None) == -1
+    # a workspace below one (batch, KV-head) group's band (here half of the
+    # band: B = 1, Hkv = 2) is rejected; between that and the whole band the
+    # call would run in passes
+    assert lib.flexatt_bwd_ws(p, t, t, t, t, t, FAKE, FAKE, t, t, t, FAKE, band // 2 - 1, None) == -1
+    assert lib.flexatt_bwd_ws(p, t, t, t, t, t, FAKE, FAKE, t, t, t, None, band, None) == -1
+    assert lib.flexatt_bwd_ws(p, t, t, t, t, t, FAKE, FAKE, t, t, t, FAKE + 8, band, None) == -5
     assert lib.flexatt_bwd_ws(p, t, t, t, t, t, FAKE, FAKE, tens(stride_h=0, stride_s=128), t, t, FAKE, need,
                               None) == -5
+
+
+@pytest.mark.parametrize("B,hq,hkv", [(2, 6, 2), (1, 8, 8), (3, 4, 1), (2, 32, 8)])
+@pytest.mark.parametrize("sq,skv,causal,window", [(4096, 4096, 1, 0), (300, 129, 0, 0), (1000, 1000, 1, 100)])
+def test_bwd_workspace_limited_plan(B, hq, hkv, sq, skv, causal, window):
+    """flexatt_bwd_workspace_limited under a byte budget: the whole band when it
+    fits; else the band of the most whole (batch, KV-head) groups that fit,
+    rounded down to whole batches when at least one batch fits; else 0 (the
+    recomputing backward).  A group's band is G query heads' units x 8 KB."""
+    lib = L.load()
+    p = problem(batch=B, heads_q=hq, heads_kv=hkv, seqlen_q=sq, seqlen_kv=skv, head_dim=128, causal=causal,
+                sliding_window=window)
+    q = L.BWD_QUEUE_BYTES
+    full = lib.flexatt_bwd_workspace(p)
+    gb = (hq // hkv) * _staged_units(sq, skv, causal, window) * 8192
+    assert full == B * hkv * gb + q
+    lim = lib.flexatt_bwd_workspace_limited
+    assert lim(p, full) == full and lim(p, 1 << 62) == full
+    assert lim(p, gb + q - 1) == 0 and lim(p, 0) == 0
+    assert lim(p, gb + q) == (gb + q if B * hkv > 1 else full)
+    for groups in range(1, B * hkv):
+        want = groups if groups < hkv else groups // hkv * hkv
+        assert lim(p, groups * gb + q) == want * gb + q, groups
+        assert lim(p, groups * gb + q + gb - 1) == want * gb + q, groups
+    # fp32 stages 4 bytes per pair: twice the bytes per group
+    p32 = problem(batch=B, heads_q=hq, heads_kv=hkv, seqlen_q=sq, seqlen_kv=skv, head_dim=128, causal=causal,
+                  sliding_window=window, dtype=L.F32)
+    if B * hkv > 1:
+        assert lim(p32, 2 * gb + q) == 2 * gb + q
+        assert lim(p32, 2 * gb + q - 1) == 0
+    # outside the staged range (head_dim 32 fp16/bf16), or an invalid problem: 0
+    assert lim(problem(head_dim=32), 1 << 40) == 0 and lim(problem(heads_q=3), 1 << 40) == 0
+
+
+def test_backward_selects_staging_within_the_limit(monkeypatch):
+    """The Python layer's choice for one backward call: the staged backward
+    with the workspace flexatt_bwd_workspace_limited gives under
+    ds_workspace_limit (whole band or one chunk of groups), the recomputing
+    backward (0) when not even one group's band fits, or when staging is off."""
+    import npu_flash_attention as nfa
+
+    lib = L.load()
+    p = problem(batch=2, heads_q=32, heads_kv=8, seqlen_q=4096, seqlen_kv=4096, head_dim=128, causal=1)
+    full = lib.flexatt_bwd_workspace(p)
+    gb = 4 * _staged_units(4096, 4096, 1, 0) * 8192
+    assert nfa.ds_workspace_limit == 4 << 30 and full < nfa.ds_workspace_limit
+    assert nfa._staged_workspace_bytes(lib, p) == full  # the bench workload runs in one pass
+    monkeypatch.setattr(nfa, "ds_workspace_limit", full - 1)
+    assert nfa._staged_workspace_bytes(lib, p) == 8 * gb + L.BWD_QUEUE_BYTES  # one batch per pass
+    monkeypatch.setattr(nfa, "ds_workspace_limit", 3 * gb + L.BWD_QUEUE_BYTES)
+    assert nfa._staged_workspace_bytes(lib, p) == 3 * gb + L.BWD_QUEUE_BYTES  # three KV heads per pass
+    monkeypatch.setattr(nfa, "ds_workspace_limit", gb)
+    assert nfa._staged_workspace_bytes(lib, p) == 0  # recomputing backward
+    monkeypatch.setattr(nfa, "ds_workspace_limit", -5)
+    assert nfa._staged_workspace_bytes(lib, p) == 0
+    monkeypatch.setattr(nfa, "ds_workspace_limit", 1 << 40)
+    monkeypatch.setattr(nfa, "ds_staging_enabled", False)
+    assert nfa._staged_workspace_bytes(lib, p) == 0
+    # B=1 Hq=32 S=64k causal bf16: 137 GB of band, 17 GB per group: recompute at the default limit
+    big = problem(batch=1, heads_q=32, heads_kv=8, seqlen_q=65536, seqlen_kv=65536, head_dim=128, causal=1)
+    monkeypatch.setattr(nfa, "ds_staging_enabled", True)
+    monkeypatch.setattr(nfa, "ds_workspace_limit", 4 << 30)
+    assert lib.flexatt_bwd_workspace(big) > 130e9
+    assert nfa._staged_workspace_bytes(lib, big) == 0

@@ -127,14 +127,26 @@ def test_config5_gqa7_reduced(gpu_device):
     print("[config5 Sq=2049] " + " ".join(f"{k}={v:.2e}" for k, v in rep.items()))
 
 
-def test_config3_full_size(gpu_device):
-    """configs[2], the bench workload, at full size: bf16 B=2 Hq=32 Hkv=8 S=4096 D=128 causal.
-    The whole problem runs on the GPU; the oracle checks one (batch, KV-head) group."""
+@pytest.fixture(scope="module")
+def config3_full():
+    """configs[2], the bench workload, at full size: bf16 B=2 Hq=32 Hkv=8
+    S=4096 D=128 causal, the whole problem on the GPU (outputs moved to the
+    CPU once for every group check)."""
     cpu, dev = draw(42, 2, 32, 8, 4096, 4096, 128, torch.bfloat16)
     got = fwd_bwd(nfa, *dev, causal=True)
     for x in got:
         assert bool(torch.isfinite(x).all())
-    bi, hk, g = 1, 5, 4
+    return cpu, [x.cpu() for x in got]
+
+
+# (batch, KV head) groups spread over the grid: the work order gives each XCD
+# two whole groups (flexatt_device.h xcd_lpt_item), so these land on
+# different XCDs and in both batches
+@pytest.mark.parametrize("bi,hk", [(0, 0), (0, 7), (1, 0), (1, 5), (1, 7)])
+def test_config3_full_size(gpu_device, config3_full, bi, hk):
+    """The oracle checks one (batch, KV-head) group of the full-size run."""
+    cpu, got = config3_full
+    g = 4
     hs = slice(hk * g, (hk + 1) * g)
     part = [t[bi:bi + 1, hs] if t.shape[1] == 32 else t[bi:bi + 1, hk:hk + 1] for t in cpu]
     ref = orc.forward_backward_chunked(*part, causal=True, dtype=torch.float32)[0][2:]
@@ -143,4 +155,4 @@ def test_config3_full_size(gpu_device):
     rep = {}
     for name, x, r in zip(NAMES, sel, ref):
         check(name, x, r, torch.bfloat16, rep)
-    print("[config3 full, group (1, 5)] " + " ".join(f"{k}={v:.2e}" for k, v in rep.items()))
+    print(f"[config3 full, group ({bi}, {hk})] " + " ".join(f"{k}={v:.2e}" for k, v in rep.items()))

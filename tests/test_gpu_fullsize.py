@@ -36,16 +36,33 @@ def _group_check(tag, dtype, got, cpu, hk, g, kw, slopes=None):
     print(f"[{tag}, group (0, {hk})] " + " ".join(f"{k_}={v_:.2e}" for k_, v_ in rep.items()))
 
 
-def test_config4_full_size(gpu_device):
-    kw = dict(causal=True, sliding_window=4096, soft_cap=50.0, scale=1.0 / 16)
+C4_KW = dict(causal=True, sliding_window=4096, soft_cap=50.0, scale=1.0 / 16)
+C5_KW = dict(causal=True, sliding_window=2048, soft_cap=30.0, scale=0.05)
+
+
+@pytest.fixture(scope="module")
+def config4_full():
     cpu, dev = draw(42, 1, 16, 8, 8192, 8192, 256, torch.bfloat16, scale_inputs=2.0)
-    got = fwd_bwd(nfa, *dev, **kw)
-    _group_check("config4 full", torch.bfloat16, got, cpu, hk=3, g=2, kw=kw)
+    got = fwd_bwd(nfa, *dev, **C4_KW)
+    return cpu, [x.cpu() for x in got]
 
 
-def test_config5_full_size(gpu_device):
+@pytest.fixture(scope="module")
+def config5_full():
     slopes = alibi_slopes(28)
-    kw = dict(causal=True, sliding_window=2048, soft_cap=30.0, scale=0.05)
     cpu, dev = draw(42, 1, 28, 4, 16384, 16383, 64, torch.float16)
-    got = fwd_bwd(nfa, *dev, alibi_slope=slopes.to(gpu_device), **kw)
-    _group_check("config5 full", torch.float16, got, cpu, hk=2, g=7, kw=kw, slopes=slopes)
+    got = fwd_bwd(nfa, *dev, alibi_slope=slopes.to("cuda"), **C5_KW)
+    return cpu, [x.cpu() for x in got], slopes
+
+
+# two KV heads each, at both ends of the head range (different XCDs)
+@pytest.mark.parametrize("hk", [0, 7])
+def test_config4_full_size(gpu_device, config4_full, hk):
+    cpu, got = config4_full
+    _group_check("config4 full", torch.bfloat16, got, cpu, hk=hk, g=2, kw=C4_KW)
+
+
+@pytest.mark.parametrize("hk", [0, 3])
+def test_config5_full_size(gpu_device, config5_full, hk):
+    cpu, got, slopes = config5_full
+    _group_check("config5 full", torch.float16, got, cpu, hk=hk, g=7, kw=C5_KW, slopes=slopes)

@@ -114,9 +114,11 @@ def test_masks_match_oracle(gpu_device, case):
         assert (o[0, 0, 128:256] == 0).all() and (dq[0, 0, 128:256] == 0).all()
 
 
-@pytest.mark.parametrize("case", ["bf16_d128_prefix", "bf16_d128_blocks_causal_dead", "bf16_d128_prefix_blocks_doc"])
+@pytest.mark.parametrize("case", ["bf16_d128_prefix", "bf16_d128_blocks_causal_dead", "bf16_d128_prefix_blocks_doc",
+                                  "fp32_d64_prefix_doc", "fp32_d128_blocks", "fp32_d64_blocks_long"])
 def test_masks_recompute_dq_kernel(gpu_device, case):
-    """The D = 128 backward without dS staging (the recomputing dQ kernel)."""
+    """The backward without dS staging (the recomputing dQ kernels: D = 128
+    fp16/bf16 and the fp32 kernels)."""
     dtype, cpu, (q, k, v, do), kw, ref = _setup(case, seed=1)
     nfa.ds_staging_enabled = False
     try:

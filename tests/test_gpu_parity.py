@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import npu_flash_attention as nfa
-from gpu_helpers import TOL, alibi_slopes, check, draw, fwd_bwd, oracle_fwd_bwd
+from gpu_helpers import TOL, alibi_slopes, check, draw, fp32_score_factor, fwd_bwd, oracle_fwd_bwd
 
 pytestmark = pytest.mark.gpu
 
@@ -101,6 +101,28 @@ def test_fp32_several_tiles(gpu_device, d, flags):
         check(name, x, r, torch.float32)
 
 
+@pytest.mark.parametrize("flags", ["causal", "window", "causal_alibi_cap", "all"])
+@pytest.mark.parametrize("d", HEAD_DIMS)
+def test_fp32_recompute_path(gpu_device, d, flags):
+    # The fp32 backward without a dS workspace (flexatt_bwd: dQ recomputes S
+    # and dP with 16 query rows per wave, dK/dV without dS stores), which the
+    # staged default never runs: G = 3, B = 2, Sq != Skv off the tile grid,
+    # several work items per head.
+    causal, window, alibi, cap, scale = FLAGS[flags]
+    window = 70 if window else 0
+    cpu, dev = draw(31, 2, 6, 2, 300, 277, d, torch.float32)
+    slopes = alibi_slopes(6) if alibi else None
+    kw = dict(causal=causal, sliding_window=window, soft_cap=cap, scale=scale)
+    nfa.ds_staging_enabled = False
+    try:
+        got = fwd_bwd(nfa, *dev, alibi_slope=None if slopes is None else slopes.to(gpu_device), **kw)
+    finally:
+        nfa.ds_staging_enabled = True
+    ref = oracle_fwd_bwd(*cpu, alibi_slope=slopes, **kw)
+    for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
+        check(name, x, r, torch.float32)
+
+
 @pytest.mark.parametrize("case", ["bf16_g8_causal_window", "fp16_g3_alibi_noncausal"])
 def test_d256_head_groups(gpu_device, case):
     # The D = 256 forward's wave pairs pack gp = min(G & -G, 4) heads per
@@ -134,6 +156,23 @@ def test_relative_position_score_mod(gpu_device, dtype):
         ref = oracle_fwd_bwd(*cpu, causal=causal, sliding_window=window, scale=0.1, alibi_slope=ones)
         for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
             check(name, x, r, dtype)
+
+
+def test_relative_position_long_fp32(gpu_device):
+    # The same score_mod over 600 positions: the bias reaches 599, and the
+    # fp32 bound scales with the largest attended score (fp32_score_factor):
+    # exp(x - m) inherits the half-ulp rounding of a score x, which grows
+    # with |x|.
+    hq = 4
+    cpu, dev = draw(24, 1, hq, 2, 600, 600, 64, torch.float32)
+    ones = torch.ones(hq, dtype=torch.float32)
+    for causal, window in ((True, 0), (False, 0)):
+        got = fwd_bwd(nfa, *dev, causal=causal, sliding_window=window, scale=0.1, alibi_slope=ones.to(gpu_device))
+        ref = oracle_fwd_bwd(*cpu, causal=causal, sliding_window=window, scale=0.1, alibi_slope=ones)
+        f = fp32_score_factor(cpu[0], cpu[1], scale=0.1, alibi_slope=ones, causal=causal, sliding_window=window)
+        assert f > 5.0
+        for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
+            check(name, x, r, torch.float32, factor=f)
 
 
 def test_fully_masked_rows(gpu_device):
