@@ -79,7 +79,8 @@ struct KvCfg {
   static constexpr int STAGES = D == 64 ? 5 : (D == 128 ? 6 : 4);
   static constexpr int WPE = D == 64 ? 4 : 2;      // waves per SIMD the register budget targets
   static constexpr int AHEAD = STAGES - 2;         // tile u + AHEAD is copied in step u
-  // D = 256 runs dV and dK in two passes (two launches), so that the KV-wave
+  // D = 256 runs dV and dK in two passes (the dV items and the dK items of one
+  // launch, bwd_kv_passes_kernel), so that the KV-wave
   // holds one 128-register accumulator set; each pass exchanges one packed
   // operand (P, or dS) instead of both
   static constexpr bool PASSES = D == 256;
@@ -97,9 +98,10 @@ struct KvCfg {
 // staged dS when DS).  TPS: tiles per step (two: both phases of a step run
 // two consecutive tiles of the walk, 32 MFMAs per wave and phase, with one
 // exchange buffer; D = 128 without block maps).
+// The tile stream of one work item: KV block kb of (b, hkv) = bh, walked as
+// workgroup slot `slot` (which sets the walk direction), in the LDS at smem.
 template <class T, int D, bool SOFTCAP, bool ALIBI, bool DS, int PASS, bool BLK, int TPS = 1>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(KvCfg<D>::WPE, KvCfg<D>::WPE)))
-void bwd_kv_kernel(BwdArgs a) {
+__device__ __forceinline__ void kv_tile_stream(const BwdArgs& a, char* smem, int slot, int kb, int bh) {
   using C = KvCfg<D, TPS>;
   static_assert(TPS == 1 || (TPS == 2 && PASS == 0 && !BLK && D == 128), "two tiles per step: D = 128, no block maps");
   static_assert(C::DB == 2 * C::KC / 4 && (D == 64 || D == 128 || D == 256), "head dims 64, 128, 256");
@@ -118,7 +120,6 @@ void bwd_kv_kernel(BwdArgs a) {
   constexpr int RAK = (D == 64 && !SOFTCAP) ? 3 : 4;
   using M = Mfma<T>;
   using V8 = typename M::v8;
-  __shared__ __attribute__((aligned(1024))) char smem[C::LDSB];
 
   const Shape& p = a.p;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -126,18 +127,7 @@ void bwd_kv_kernel(BwdArgs a) {
   const int pr = wave & (C::NP - 1);  // pair: KV rows [32 pr, 32 pr + 32) of the block
   const bool s_wave = wave < C::NP;
   const int h = lane >> 5, l32 = lane & 31;
-
-  // Work item: (b, hkv, KV block), blocks of one (b, hkv) consecutive so that
-  // they share an XCD (and its L2) and heavy / light causal blocks interleave.
   const int nkb = a.ntiles;
-  const int slot = queue_slot(a.queue, a.nstatic);
-  if (slot >= (int)gridDim.x) return;  // (a counter that was not cleared)
-  int kb, bh;  // block 0 has the longest causal band
-  if (!xcd_lpt_item(slot, nkb, p.B * p.Hkv, kb, bh)) {
-    const int w = xcd_remap(slot, gridDim.x);
-    kb = w % nkb;
-    bh = w / nkb;
-  }
   const int hk = bh % p.Hkv, b = bh / p.Hkv;
   const int n0 = kb * C::BKV;
   const int kw0 = n0 + 32 * pr;  // first KV row of this pair
@@ -953,6 +943,51 @@ void bwd_kv_kernel(BwdArgs a) {
   }
 }
 
+// D = 64 and 128 (PASS 0).  Work item: (b, hkv, KV block), blocks of
+// one (b, hkv) consecutive so that they share an XCD (and its L2) and heavy /
+// light causal blocks interleave; block 0 has the longest causal band.
+template <class T, int D, bool SOFTCAP, bool ALIBI, bool DS, int PASS, bool BLK, int TPS = 1>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(KvCfg<D>::WPE, KvCfg<D>::WPE)))
+void bwd_kv_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) char smem[KvCfg<D, TPS>::LDSB];
+  const int nkb = a.ntiles;
+  const int slot = queue_slot(a.queue, a.nstatic);
+  if (slot >= (int)gridDim.x) return;  // (a counter that was not cleared)
+  int kb, bh;
+  if (!xcd_lpt_item(slot, nkb, a.p.B * a.p.Hkv, kb, bh)) {
+    const int w = xcd_remap(slot, gridDim.x);
+    kb = w % nkb;
+    bh = w / nkb;
+  }
+  kv_tile_stream<T, D, SOFTCAP, ALIBI, DS, PASS, BLK, TPS>(a, smem, slot, kb, bh);
+}
+
+// D = 256: the dV pass (PASS 1) and the dK pass (PASS 2) of every KV block in
+// one launch, 2 nkb items per (b, hkv), so that the work order deals both
+// passes' items longest first over the CUs together.  With one launch per
+// pass each launch ends with its own tail: a windowed band puts its many
+// equal-length items in the first round and the truncated ones after them
+// (at config 4, 132 query tiles then 128 .. 4 per CU, against 99 on average).
+// Item k of a group: KV block k / 2, the dK pass for even k (the longer of the
+// two per tile: dP MFMAs and the staged dS stores) and the dV pass for odd k.
+template <class T, int D, bool SOFTCAP, bool ALIBI, bool DS, bool BLK>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(KvCfg<D>::WPE, KvCfg<D>::WPE)))
+void bwd_kv_passes_kernel(BwdArgs a) {
+  static_assert(KvCfg<D>::PASSES, "two passes at D = 256 only");
+  __shared__ __attribute__((aligned(1024))) char smem[KvCfg<D>::LDSB];
+  const int nit = 2 * a.ntiles;  // items per (b, hkv)
+  const int slot = queue_slot(a.queue, a.nstatic);
+  if (slot >= (int)gridDim.x) return;  // (a counter that was not cleared)
+  int k, bh;
+  if (!xcd_lpt_item(slot, nit, a.p.B * a.p.Hkv, k, bh)) {
+    const int w = xcd_remap(slot, gridDim.x);
+    k = w % nit;
+    bh = w / nit;
+  }
+  if ((k & 1) == 0) kv_tile_stream<T, D, SOFTCAP, ALIBI, DS, 2, BLK>(a, smem, slot, k >> 1, bh);
+  else kv_tile_stream<T, D, SOFTCAP, ALIBI, false, 1, BLK>(a, smem, slot, k >> 1, bh);
+}
+
 #ifndef FLEXATT_KV_TPS
 #define FLEXATT_KV_TPS 2  // tiles per step at D = 128 without block maps (tuning override; 1.7% faster than 1)
 #endif
@@ -968,7 +1003,7 @@ hipError_t launch_kv(const BwdArgs& a, hipStream_t st) {
   auto go = [&](auto pass_c) {
     constexpr int PS = decltype(pass_c)::value;
     constexpr bool DSP = DS && PS != 1;
-    x.queue = a.queue ? a.queue + (PS == 2 ? 1 : 0) : nullptr;  // one counter per launch
+    x.queue = a.queue;
     // block-sparse maps: the walk list of live query tiles in dynamic LDS
     // (when it fits beside the tile stages; otherwise removed tiles are walked
     // and only their S-wave work is skipped)
@@ -997,9 +1032,25 @@ hipError_t launch_kv(const BwdArgs& a, hipStream_t st) {
     return hipGetLastError();
   };
   if constexpr (C::PASSES) {
-    const hipError_t e = go(std::integral_constant<int, 1>{});
-    if (e != hipSuccess) return e;
-    return go(std::integral_constant<int, 2>{});
+    {
+      // both passes in one launch (bwd_kv_passes_kernel)
+      const dim3 grid2(2 * x.ntiles * a.p.B * a.p.Hkv);
+      x.queue = a.queue;
+      const size_t dyn = 2 * (size_t)((a.p.Sq + C::BM - 1) / C::BM + 2);
+      const bool blk = a.p.blk && C::LDSB + dyn <= 160 * 1024;
+      if (blk) {
+        if (sc && al) hipLaunchKernelGGL((bwd_kv_passes_kernel<T, D, true, true, DS, true>), grid2, block, dyn, st, x);
+        else if (sc) hipLaunchKernelGGL((bwd_kv_passes_kernel<T, D, true, false, DS, true>), grid2, block, dyn, st, x);
+        else if (al) hipLaunchKernelGGL((bwd_kv_passes_kernel<T, D, false, true, DS, true>), grid2, block, dyn, st, x);
+        else hipLaunchKernelGGL((bwd_kv_passes_kernel<T, D, false, false, DS, true>), grid2, block, dyn, st, x);
+      } else {
+        if (sc && al) hipLaunchKernelGGL((bwd_kv_passes_kernel<T, D, true, true, DS, false>), grid2, block, 0, st, x);
+        else if (sc) hipLaunchKernelGGL((bwd_kv_passes_kernel<T, D, true, false, DS, false>), grid2, block, 0, st, x);
+        else if (al) hipLaunchKernelGGL((bwd_kv_passes_kernel<T, D, false, true, DS, false>), grid2, block, 0, st, x);
+        else hipLaunchKernelGGL((bwd_kv_passes_kernel<T, D, false, false, DS, false>), grid2, block, 0, st, x);
+      }
+      return hipGetLastError();
+    }
   } else {
     return go(std::integral_constant<int, 0>{});
   }

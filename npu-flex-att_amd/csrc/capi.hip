@@ -617,7 +617,7 @@ int run_staged(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_
                const flexatt_tensor* o, const flexatt_tensor* dout, const float* lse, float* delta,
                const flexatt_tensor* dq, const flexatt_tensor* dk, const flexatt_tensor* dv, void* workspace,
                size_t workspace_bytes, void* stream) {
-  // queue counters after the dS band: [0], [1] the dK/dV launches, [2] dQ
+  // queue counters after the dS band: [0] the dK/dV launch, [2] dQ
   int* queue = nullptr;
   if (workspace_bytes >= ds_bytes(p) + FLEXATT_BWD_QUEUE_BYTES && (cu_count() & ~7) > 0)
     queue = (int*)((char*)workspace + ds_bytes(p));

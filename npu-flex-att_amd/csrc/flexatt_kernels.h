@@ -96,7 +96,7 @@ hipError_t bwd_kv_bf16_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_f16_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_bf16_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_kv_f16_d64(const BwdArgs&, hipStream_t);
-hipError_t bwd_kv_bf16_d256(const BwdArgs&, hipStream_t);  // two launches: dV, then dK
+hipError_t bwd_kv_bf16_d256(const BwdArgs&, hipStream_t);  // dV and dK passes as items of one launch
 hipError_t bwd_kv_f16_d256(const BwdArgs&, hipStream_t);
 
 // dK/dV that also writes its dS to a.ds (bwd_kv.hip), and dQ = scale * dS K
