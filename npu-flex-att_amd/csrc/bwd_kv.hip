@@ -715,12 +715,13 @@ __device__ __forceinline__ void kv_tile_stream(const BwdArgs& a, char* smem, int
     // work anyway (3% faster there), in M(u) at D = 64 (3% faster there); the
     // tile waits count the stores either way, as they precede them.
     constexpr bool DS_LATE = D != 64;
-    auto store_ds = [&](const i16x4 (&st4)[4]) {
-      // streamed past the caches: each fragment is read once, by the dQ kernel
-#pragma unroll
-      for (int f = 0; f < 2; ++f)
-        __builtin_nontemporal_store(__builtin_bit_cast(i32x4, cat_tr<V8>(st4[2 * f], st4[2 * f + 1])),
-                                    (i32x4*)(dsp + f * 1024));
+    // fragment f of the staged dS, streamed past the caches: each fragment
+    // is read once, by the dQ kernel
+    auto store_frag = [&](const i16x4 (&st4)[4], int f) {
+      __builtin_nontemporal_store(__builtin_bit_cast(i32x4, cat_tr<V8>(st4[2 * f], st4[2 * f + 1])),
+                                  (i32x4*)(dsp + f * 1024));
+    };
+    auto ds_next = [&]() {  // the unit cursor to the next tile
       if constexpr (BLK) {
         if (++su < ntile) dsp = ds_at(su % p.G, qt_at(su / p.G));
         return;
@@ -741,12 +742,17 @@ __device__ __forceinline__ void kv_tile_stream(const BwdArgs& a, char* smem, int
       }
       dsp += step * kDsUnitB;
     };
+    auto store_ds = [&](const i16x4 (&st4)[4]) {
+      store_frag(st4, 0);
+      store_frag(st4, 1);
+      ds_next();
+    };
     if constexpr (TPS > 1) {
       // Step u: the dV / dK MFMAs of step u-1's tiles (TPS (u-1) + w, in
       // stages s_tr2 + w) in V(u); the copies of step u+1's tiles in M(u),
       // into the stages of step u-2's tiles (read in V(u-1)); so each copy
       // has one step to land.  The staged dS of step u-1's live tiles leaves
-      // after the MFMAs, and the wait at the end of V(u) lets only those
+      // between the MFMAs, and the wait at the end of V(u) lets only those
       // stores stay in flight.
       const int nstep = (ntile + TPS - 1) / TPS;
       int s_cp2 = 0;  // stage of the next tile to copy
@@ -819,13 +825,22 @@ __device__ __forceinline__ void kv_tile_stream(const BwdArgs& a, char* smem, int
             const V8 av = cat_tr<V8>(blo[jj % (RAK + 1)], bhi[jj % (RAK + 1)]);
             if (isk) dk[db] = M::mma(av, PS[w][qc], dk[db]);
             else dv[db] = M::mma(av, PP[w][qc], dv[db]);
+            if constexpr (DS) {
+              // fragment f of tile t leaves after MFMA 3 + 8 (2 t + f): the
+              // KV-waves' stores spread over the phase instead of meeting
+              // at its end (1% faster than all four after the MFMAs; other
+              // spacings measured slower)
+              static_assert(TPS * NJ == 32, "four stores over 32 MFMAs");
+              if (jj % 8 == 3) {
+                const int t = jj >> 4, f = (jj >> 3) & 1;
+                if (t < na) {
+                  store_frag(st4[t], f);
+                  if (f == 1) ds_next();
+                }
+              }
+            }
           }
           __builtin_amdgcn_sched_barrier(0);
-          if constexpr (DS) {
-#pragma unroll
-            for (int w = 0; w < TPS; ++w)
-              if (w < na) store_ds(st4[w]);
-          }
           s_tr2 += TPS;
           if (s_tr2 >= C::STAGES) s_tr2 -= C::STAGES;
         }
