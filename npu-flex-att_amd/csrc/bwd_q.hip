@@ -43,7 +43,7 @@
 
 namespace flexatt {
 
-#if FLEXATT_D == 128
+#if FLEXATT_D == 128 || FLEXATT_D == 64
 
 template <int D>
 struct QCfg {
@@ -61,7 +61,8 @@ struct QCfg {
   static constexpr int RA = 4;  // row reads issued this many MFMAs ahead
   static constexpr int RB = 3;  // transpose reads issued this many dQ MFMAs ahead
   static_assert(E * 1024 * NW == TILEB, "tile must split into 1 KB copies");
-  static_assert(NS * 64 * 64 * 4 <= STAGES * STAGEB, "the partial-dQ exchange fits in the stage memory");
+  static_assert(4 * DB * NS * 64 * 16 <= STAGES * STAGEB, "the partial-dQ exchange fits in the stage memory");
+  static_assert(2 * DB == KC, "the dQ MFMAs of a tile (2 DB) interleave with its S / dP MFMAs (2 KC)");
 };
 
 template <class T, int D, bool SOFTCAP, bool ALIBI>
@@ -70,7 +71,7 @@ void bwd_q_kernel(BwdArgs a) {
   using C = QCfg<D>;
   using M = Mfma<T>;
   using V8 = typename M::v8;
-  static_assert(C::KC == 8 && C::DB == 4, "the phase layout assumes D = 128");
+  static_assert(D == 128 || D == 64, "head dims 64 and 128");
   __shared__ __attribute__((aligned(1024))) char smem[C::STAGES * C::STAGEB];
 
   const Shape& p = a.p;
@@ -318,17 +319,17 @@ void bwd_q_kernel(BwdArgs a) {
       for (int j = 0; j < RB; ++j) rdB(j, blo[j], bhi[j]);
     }
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
+    for (int k = 0; k < 2 * C::KC; ++k) {
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (DO_S) {
-        if (k + RA < 16) ab[(k + RA) % (RA + 1)] = rdA(k + RA);
+        if (k + RA < 2 * C::KC) ab[(k + RA) % (RA + 1)] = rdA(k + RA);
         if (k & 1) DP = M::mma(as_v8<V8>(ab[k % (RA + 1)]), df[k >> 1], DP);
         else S = M::mma(as_v8<V8>(ab[k % (RA + 1)]), qf[k >> 1], S);
       }
       if constexpr (DO_Q) {
         if (k & 1) {
           const int j = k >> 1;
-          if (j + RB < 8) rdB(j + RB, blo[(j + RB) % (RB + 1)], bhi[(j + RB) % (RB + 1)]);
+          if (j + RB < C::KC) rdB(j + RB, blo[(j + RB) % (RB + 1)], bhi[(j + RB) % (RB + 1)]);
           const int db = j % C::DB, c16 = j / C::DB;
           dq[db] = M::mma(cat_tr<V8>(blo[j % (RB + 1)], bhi[j % (RB + 1)]), PS[c16], dq[db]);
         }
@@ -418,9 +419,14 @@ hipError_t launch_q(const BwdArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+#if FLEXATT_D == 128
 hipError_t bwd_q_bf16_d128(const BwdArgs& a, hipStream_t st) { return launch_q<__bf16, 128>(a, st); }
 hipError_t bwd_q_f16_d128(const BwdArgs& a, hipStream_t st) { return launch_q<_Float16, 128>(a, st); }
+#else
+hipError_t bwd_q_bf16_d64(const BwdArgs& a, hipStream_t st) { return launch_q<__bf16, 64>(a, st); }
+hipError_t bwd_q_f16_d64(const BwdArgs& a, hipStream_t st) { return launch_q<_Float16, 64>(a, st); }
+#endif
 
-#endif  // FLEXATT_D == 128
+#endif  // FLEXATT_D == 128 || FLEXATT_D == 64
 
 }  // namespace flexatt

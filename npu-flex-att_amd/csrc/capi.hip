@@ -135,8 +135,8 @@ const FwdLauncher kFwd[3][4] = {
 };
 const BwdLauncher kDq[3][4] = {
     {bwd_dq_f32_d32, bwd_dq_f32_d64, bwd_dq_f32_d128, bwd_dq_f32_d256},
-    {bwd_dq_mfma_f16_d32, bwd_dq_mfma_f16_d64, bwd_q_f16_d128, bwd_dq_mfma_f16_d256},
-    {bwd_dq_mfma_bf16_d32, bwd_dq_mfma_bf16_d64, bwd_q_bf16_d128, bwd_dq_mfma_bf16_d256},
+    {bwd_dq_mfma_f16_d32, bwd_q_f16_d64, bwd_q_f16_d128, bwd_dq_mfma_f16_d256},
+    {bwd_dq_mfma_bf16_d32, bwd_q_bf16_d64, bwd_q_bf16_d128, bwd_dq_mfma_bf16_d256},
 };
 const BwdLauncher kDkdv[3][4] = {
     {bwd_dkdv_f32_d32, bwd_dkdv_f32_d64, bwd_dkdv_f32_d128, bwd_dkdv_f32_d256},
@@ -240,13 +240,19 @@ int scratch_for_stream(hipStream_t stream, void** out) {
 // D = 128 tile stream has neither); the D = 128 dK/dV tile stream has both.
 bool has_masks(const flexatt_problem* p) { return p->doc_bounds || p->block_map; }
 BwdLauncher pick_dq(const flexatt_problem* p) {
-  if (has_masks(p) && p->head_dim == 128 && p->dtype != FLEXATT_F32)
-    return p->dtype == FLEXATT_BF16 ? bwd_dq_mfma_bf16_d128 : bwd_dq_mfma_f16_d128;
+  // the query-stationary tile stream (bwd_q.hip) has no document, prefix or
+  // block-map masks: with them the general kernel runs
+  if (has_masks(p) && p->dtype != FLEXATT_F32) {
+    const bool bf = p->dtype == FLEXATT_BF16;
+    if (p->head_dim == 128) return bf ? bwd_dq_mfma_bf16_d128 : bwd_dq_mfma_f16_d128;
+    if (p->head_dim == 64) return bf ? bwd_dq_mfma_bf16_d64 : bwd_dq_mfma_f16_d64;
+  }
   return kDq[p->dtype][head_index(p->head_dim)];
 }
-// The dQ kernel that can also form Delta itself (the D = 128 tile stream).
+// The dQ kernel that can also form Delta itself (the D = 64 and 128 tile stream).
 bool dq_fuses_delta(const flexatt_problem* p) {
-  return pick_dq(p) == (p->dtype == FLEXATT_BF16 ? bwd_q_bf16_d128 : bwd_q_f16_d128);
+  const BwdLauncher f = pick_dq(p);
+  return f == bwd_q_bf16_d128 || f == bwd_q_f16_d128 || f == bwd_q_bf16_d64 || f == bwd_q_f16_d64;
 }
 BwdLauncher pick_dkdv(const flexatt_problem* p) { return kDkdv[p->dtype][head_index(p->head_dim)]; }
 

@@ -138,9 +138,11 @@ hipError_t bwd_dq_ds_f32_d64(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_f32_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_dq_ds_f32_d256(const BwdArgs&, hipStream_t);
 
-// dQ as a query-stationary tile stream (bwd_q.hip), D = 128; with
+// dQ as a query-stationary tile stream (bwd_q.hip), D = 64 and 128; with
 // a.delta_out set it also computes Delta (written there) from O and dO.
 hipError_t bwd_q_bf16_d128(const BwdArgs&, hipStream_t);
 hipError_t bwd_q_f16_d128(const BwdArgs&, hipStream_t);
+hipError_t bwd_q_bf16_d64(const BwdArgs&, hipStream_t);
+hipError_t bwd_q_f16_d64(const BwdArgs&, hipStream_t);
 
 }  // namespace flexatt

@@ -1,5 +1,5 @@
 """GPU tests of flexatt_bwd_dq_delta, the entry point that forms Delta inside
-the dQ kernel (D = 128 fp16/bf16) instead of in a separate pass.
+the dQ kernel (D = 64 and 128 fp16/bf16) instead of in a separate pass.
 
 Against the separate passes (flexatt_bwd_delta, then flexatt_bwd_dq) on the
 same inputs: Delta agrees to fp32 summation-order rounding, dQ within the
@@ -25,7 +25,8 @@ CASES = {
     "fp16_d128_all": (torch.float16, 128, 8, 4, 333, 257,
                       dict(causal=True, sliding_window=97, soft_cap=20.0, scale=0.06, alibi=True)),
     "bf16_d128_noncausal_ragged": (torch.bfloat16, 128, 4, 4, 129, 77, dict(causal=False)),
-    "bf16_d64_separate": (torch.bfloat16, 64, 8, 2, 200, 150, dict(causal=True)),
+    "fp16_d64_window_gqa": (torch.float16, 64, 6, 2, 261, 300, dict(causal=True, sliding_window=70)),
+    "bf16_d32_separate": (torch.bfloat16, 32, 8, 2, 200, 150, dict(causal=True)),
 }
 
 
@@ -61,7 +62,7 @@ def test_fused_delta_matches_separate_passes(gpu_device, case):
     scale = max(1.0, ref.abs().max().item())
     assert (delta_f.double() - ref).abs().max().item() <= 1e-5 * scale
     assert (delta_s.double() - ref).abs().max().item() <= 1e-5 * scale
-    if d == 128:
+    if d in (64, 128):
         check("dq", dq_f.float(), dq_s.float(), dtype)
     else:  # outside the fused range: the separate passes, bitwise
         assert torch.equal(delta_f, delta_s)

@@ -123,6 +123,30 @@ def test_fp32_recompute_path(gpu_device, d, flags):
         check(name, x, r, torch.float32)
 
 
+@pytest.mark.parametrize("flags", ["full", "causal", "window", "causal_alibi_cap", "all"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_recompute_path_16bit(gpu_device, dtype, d, flags):
+    # The fp16/bf16 backward without a dS workspace (flexatt_bwd: the query-
+    # stationary dQ kernel that recomputes S and dP and forms Delta itself,
+    # then dK/dV without dS stores), which the staged default runs only when
+    # even one (batch, KV-head) group's band exceeds the workspace budget:
+    # G = 3, B = 2, Sq != Skv off the tile grid, several work items per head.
+    causal, window, alibi, cap, scale = FLAGS[flags]
+    window = 70 if window else 0
+    cpu, dev = draw(37, 2, 6, 2, 300, 277, d, dtype)
+    slopes = alibi_slopes(6) if alibi else None
+    kw = dict(causal=causal, sliding_window=window, soft_cap=cap, scale=scale)
+    nfa.ds_staging_enabled = False
+    try:
+        got = fwd_bwd(nfa, *dev, alibi_slope=None if slopes is None else slopes.to(gpu_device), **kw)
+    finally:
+        nfa.ds_staging_enabled = True
+    ref = oracle_fwd_bwd(*cpu, alibi_slope=slopes, **kw)
+    for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
+        check(name, x, r, dtype)
+
+
 @pytest.mark.parametrize("case", ["bf16_g8_causal_window", "fp16_g3_alibi_noncausal"])
 def test_d256_head_groups(gpu_device, case):
     # The D = 256 forward's wave pairs pack gp = min(G & -G, 4) heads per
