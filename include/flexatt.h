@@ -151,7 +151,7 @@ int flexatt_bwd_dq(const flexatt_problem* p, const flexatt_tensor* q, const flex
                    const float* delta, const flexatt_tensor* dq, void* stream);
 
 /* Backward Delta and dQ in one pass where the dQ kernel can form Delta itself
- * (fp16/bf16, head_dim 128, no interval or block mask; otherwise the Delta
+ * (fp16/bf16, head_dim 64 or 128, no interval or block mask; otherwise the Delta
  * pass then dQ): delta (the caller's fp32 [B,Hq,Sq] buffer) receives sum_d o * dout,
  * for flexatt_bwd_dkdv after it.  Replaces the Delta op and the
  * flash_attn_bwd_dq_kernel launch of npu_flash_attention_backward,
