@@ -40,10 +40,17 @@ namespace flexatt {
 
 #if FLEXATT_D == 128 || FLEXATT_D == 64 || FLEXATT_D == 256
 
+#ifndef FLEXATT_DQ_W256
+#define FLEXATT_DQ_W256 8  // tuning override: 4 waves (one per SIMD, two slots each) at D = 256
+#endif
 template <int D>
 struct DqsCfg {
-  static constexpr int NW = 4;                 // waves per workgroup, one per SIMD
-  static constexpr int NSL = D == 256 ? 2 : 4;  // query slots per wave (256 accumulator registers at D = 256)
+  // waves per workgroup: one per SIMD (D = 64, 128); at D = 256 two per SIMD
+  // with one slot each (128 accumulators), so that one wave's loads and LDS
+  // reads overlap the other's MFMAs
+  static constexpr int NW = D == 256 ? FLEXATT_DQ_W256 : 4;
+  static constexpr int WPE = NW / 4;            // waves per SIMD
+  static constexpr int NSL = D == 256 ? 8 / NW : 4;  // query slots per wave (256 accumulators per SIMD at D = 256)
   static constexpr int SLOTS = NW * NSL;        // query slots per workgroup
   static constexpr int SB = 64;                // KV rows per sub-block
   static constexpr int KS = SB / 16;           // k steps per sub-block
@@ -62,7 +69,7 @@ struct DqsCfg {
 };
 
 template <class T, int D, bool BLK>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(DqsCfg<D>::NW * 64) __attribute__((amdgpu_waves_per_eu(DqsCfg<D>::WPE, DqsCfg<D>::WPE)))
 void bwd_dq_ds_kernel(BwdArgs a) {
   using C = DqsCfg<D>;
   using M = Mfma<T>;
@@ -234,10 +241,14 @@ void bwd_dq_ds_kernel(BwdArgs a) {
   };
   auto wait_ds = [&](i32x4 (&buf)[C::NDS], auto n_c) {
     constexpr int N = decltype(n_c)::value;
-    static_assert(C::NDS == 8 || C::NDS == 16, "dS operand count");
-    wait_vmcnt_tied<N>(buf[0], buf[1], buf[2], buf[3], buf[4], buf[5], buf[6], buf[7]);
-    if constexpr (C::NDS == 16)
-      wait_vmcnt_tied<N>(buf[8], buf[9], buf[10], buf[11], buf[12], buf[13], buf[14], buf[15]);
+    static_assert(C::NDS == 4 || C::NDS == 8 || C::NDS == 16, "dS operand count");
+    if constexpr (C::NDS == 4) {
+      wait_vmcnt_tied<N>(buf[0], buf[1], buf[2], buf[3]);
+    } else {
+      wait_vmcnt_tied<N>(buf[0], buf[1], buf[2], buf[3], buf[4], buf[5], buf[6], buf[7]);
+      if constexpr (C::NDS == 16)
+        wait_vmcnt_tied<N>(buf[8], buf[9], buf[10], buf[11], buf[12], buf[13], buf[14], buf[15]);
+    }
   };
 
   // Transpose-read offsets (A operands K^T: rows 4h + (lane % 16) / 4 and

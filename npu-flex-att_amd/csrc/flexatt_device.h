@@ -148,6 +148,10 @@ __device__ __forceinline__ void wait_vmcnt_tied(i32x4& a, i32x4& b, i32x4& c, i3
                : "n"(N)
                : "memory");
 }
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_tied(i32x4& a, i32x4& b, i32x4& c, i32x4& d) {
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
+}
 __device__ __forceinline__ unsigned lds_addr_of(const void* p) {
   return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
