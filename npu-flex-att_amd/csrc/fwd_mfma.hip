@@ -111,16 +111,15 @@ void fwd_mfma_kernel(FwdArgs a) {
   const T* kp = (const T*)a.k.data + b * a.k.sb + hk * a.k.sh;
   const T* vp = (const T*)a.v.data + b * a.v.sb + hk * a.v.sh;
 
+  // Q rows past Sq load row Sq - 1 (finite scores; their O and LSE are not
+  // stored).  Nothing reads qf before the first tile copies are issued, so
+  // the Q loads and the copies share one memory round trip.
   V8 qf[C::KC];
   {
     const int r = min(my_m, p.Sq - 1);
     const T* src = qp + (int64_t)r * a.q.ss + 8 * h;
 #pragma unroll
-    for (int kc = 0; kc < C::KC; ++kc) {
-      i32x4 x = ld_global16(src + 16 * kc);
-      if (my_m >= p.Sq) x = i32x4{0, 0, 0, 0};
-      qf[kc] = as_v8<V8>(x);
-    }
+    for (int kc = 0; kc < C::KC; ++kc) qf[kc] = as_v8<V8>(ld_global16(src + 16 * kc));
   }
 
   int kv_lo = 0, kv_hi = p.Skv;
