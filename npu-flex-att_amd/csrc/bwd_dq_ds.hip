@@ -10,19 +10,19 @@
 //
 // Decomposition
 //  * A workgroup is 4 waves, one per SIMD, for one (b, KV head) and 16 query
-//    slots (8 at D = 256; a slot is 32 rows of one query head): nh heads (4,
-//    2 or 1, the largest dividing Hq / Hkv) x slots / nh query tiles.  Wave v
-//    owns slots NSL v .. NSL v + NSL - 1 (NSL = 4, or 2 at D = 256), lane =
-//    query row; its dQ^T (NSL slots x D x 32 fp32) lives in the accumulation
-//    registers.
+//    slots, or at D = 256 8 waves, two per SIMD, and 8 slots (a slot is 32
+//    rows of one query head): nh heads (4, 2 or 1, the largest dividing
+//    Hq / Hkv) x slots / nh query tiles.  Wave v owns slots NSL v ..
+//    NSL v + NSL - 1 (NSL = 4, or 1 at D = 256), lane = query row; its dQ^T
+//    (NSL slots x D x 32 fp32) lives in the accumulation registers.
 //  * The workgroup walks the 64-row KV sub-blocks its slots' dS bands cover.
 //    K rows (16 KB per sub-block, read by all waves) go global -> LDS with
 //    direct-to-LDS loads three sub-blocks ahead into four stages; dS goes
 //    global -> registers two sub-blocks ahead, already in the MFMA B operand
 //    layout the dK/dV kernel stored it in (64 KB per sub-block and CU, read
 //    once, so 128 KB in flight per CU).
-//  * Per sub-block and wave: 64 MFMAs dQ^T += K^T dS^T; each K^T operand
-//    (two LDS transpose reads) feeds the four slots.
+//  * Per sub-block and wave: KS x DB x NSL MFMAs dQ^T += K^T dS^T; each K^T
+//    operand (two LDS transpose reads) feeds the wave's slots.
 //  * A slot whose band does not cover a sub-block skips its MFMAs and loads
 //    a valid address instead, so every wave issues the same memory
 //    operations per sub-block and fixed vmcnt waits hold.
