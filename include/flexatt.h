@@ -222,6 +222,13 @@ int flexatt_bwd(const flexatt_problem* p, const flexatt_tensor* q, const flexatt
  * give the same results as one pass up to fp32 summation order. */
 size_t flexatt_bwd_workspace(const flexatt_problem* p);
 size_t flexatt_bwd_workspace_limited(const flexatt_problem* p, size_t limit_bytes);
+/* Whether staging pays for p: 1 when p is in the staged range and the staged
+ * backward measured faster than the recomputing one on MI355X, 0 otherwise
+ * (out of range, or fp16/bf16 at head_dim 64 without soft-cap and without
+ * document, prefix or block-map masks, where the recomputing backward is
+ * 2-15% faster).  Advisory: flexatt_bwd_ws stages whenever it is given a
+ * workspace.  No counterpart in the reference, which has one backward. */
+int flexatt_bwd_prefers_staging(const flexatt_problem* p);
 int flexatt_bwd_ws(const flexatt_problem* p, const flexatt_tensor* q, const flexatt_tensor* k,
                    const flexatt_tensor* v, const flexatt_tensor* o, const flexatt_tensor* dout,
                    const float* lse, float* delta, const flexatt_tensor* dq, const flexatt_tensor* dk,
@@ -247,7 +254,7 @@ const char* flexatt_status_string(int status);
 /* ABI version of this header (bumped on any signature change). */
 int flexatt_abi_version(void);
 
-#define FLEXATT_ABI_VERSION 7
+#define FLEXATT_ABI_VERSION 8
 
 #ifdef __cplusplus
 }

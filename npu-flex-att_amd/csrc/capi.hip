@@ -563,6 +563,16 @@ size_t flexatt_bwd_workspace(const flexatt_problem* p) {
   return n ? n + FLEXATT_BWD_QUEUE_BYTES : 0;
 }
 
+int flexatt_bwd_prefers_staging(const flexatt_problem* p) {
+  if (flexatt_bwd_workspace(p) == 0) return 0;  // outside the staged range (or an invalid problem)
+  // fp16/bf16 at head_dim 64 without soft-cap and without document, prefix or
+  // block-map masks: the recomputing backward (the query-stationary dQ kernel
+  // forming Delta, dK/dV without dS stores) measured 2-15% faster than
+  // staging; with soft-cap its tanh recompute in dQ makes it 0-8% slower
+  if (p->dtype != FLEXATT_F32 && p->head_dim == 64 && !(p->soft_cap > 0.f) && !has_masks(p)) return 0;
+  return 1;
+}
+
 size_t flexatt_bwd_workspace_limited(const flexatt_problem* p, size_t limit_bytes) {
   const size_t full = flexatt_bwd_workspace(p);
   if (full == 0 || full <= limit_bytes) return full;

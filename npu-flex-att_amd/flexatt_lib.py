@@ -27,13 +27,14 @@ EXPORTS = (
     "flexatt_bwd",
     "flexatt_bwd_workspace",
     "flexatt_bwd_workspace_limited",
+    "flexatt_bwd_prefers_staging",
     "flexatt_bwd_ws",
     "flexatt_bwd_dkdv_ds",
     "flexatt_bwd_dq_ds",
     "flexatt_status_string",
     "flexatt_abi_version",
 )
-ABI_VERSION = 7
+ABI_VERSION = 8
 # Fixed scratch of flexatt_fwd_decode_noalloc (FLEXATT_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = 16 << 20
 # Work-queue counters at the end of the staged-dS workspace (FLEXATT_BWD_QUEUE_BYTES).
@@ -119,6 +120,8 @@ def load() -> ctypes.CDLL:
         getattr(lib, name).restype = ctypes.c_size_t
     lib.flexatt_bwd_workspace_limited.argtypes = [pr, ctypes.c_size_t]
     lib.flexatt_bwd_workspace_limited.restype = ctypes.c_size_t
+    lib.flexatt_bwd_prefers_staging.argtypes = [pr]
+    lib.flexatt_bwd_prefers_staging.restype = ctypes.c_int
     lib.flexatt_status_string.argtypes = [ctypes.c_int]
     lib.flexatt_status_string.restype = ctypes.c_char_p
     lib.flexatt_abi_version.argtypes = []

@@ -60,9 +60,14 @@ _DTYPES = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _li
 decode_enabled = True
 # The backward stages dS through a workspace (flexatt_bwd_ws) whenever the
 # library supports it for the problem (fp16/bf16 at head_dim 64, 128 and 256;
-# fp32 at every head_dim).  Set to False to run the recomputing dQ kernel
-# (flexatt_bwd).
+# fp32 at every head_dim) and reports that staging pays (below).  Set to
+# False to run the recomputing dQ kernel (flexatt_bwd).
 ds_staging_enabled = True
+# Stage only where flexatt_bwd_prefers_staging reports that staging pays:
+# not at head_dim 64 fp16/bf16 without soft-cap or interval/block masks,
+# where the recomputing backward measured 2-15% faster.  False: stage
+# wherever the staged range covers the problem.
+ds_staging_auto = True
 # Byte budget of that workspace for one backward call.  The whole dS band
 # (about one byte per attended (query row, key) pair of each query head for
 # fp16/bf16, two for fp32) is used when it fits; otherwise the staged backward
@@ -409,9 +414,11 @@ def _staged_workspace_bytes(lib, p) -> int:
     """Workspace bytes of the staged backward for problem ``p`` under
     ``ds_workspace_limit`` (the whole band, or the band of the chunk of whole
     (batch, KV-head) groups one pass covers); 0 selects the recomputing
-    backward (staging disabled, outside its range, or not even one group's
-    band within the limit)."""
+    backward (staging disabled, outside its range, slower for ``p`` under
+    ``ds_staging_auto``, or not even one group's band within the limit)."""
     if not ds_staging_enabled:
+        return 0
+    if ds_staging_auto and not lib.flexatt_bwd_prefers_staging(p):
         return 0
     return int(lib.flexatt_bwd_workspace_limited(p, max(0, int(ds_workspace_limit))))
 

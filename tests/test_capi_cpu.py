@@ -389,6 +389,41 @@ def test_bwd_workspace_limited_plan(B, hq, hkv, sq, skv, causal, window):
     assert lim(problem(head_dim=32), 1 << 40) == 0 and lim(problem(heads_q=3), 1 << 40) == 0
 
 
+@pytest.mark.parametrize("kw,want", [
+    (dict(head_dim=128), 1),
+    (dict(head_dim=256, soft_cap=50.0), 1),
+    (dict(head_dim=64), 0),                       # the recomputing backward is faster
+    (dict(head_dim=64, dtype=L.F16, causal=0, sliding_window=30), 0),
+    (dict(head_dim=64, soft_cap=30.0), 1),        # its tanh recompute in dQ makes it slower
+    (dict(head_dim=64, doc_bounds=FAKE), 1),      # masks: the recomputing dQ is the general kernel
+    (dict(head_dim=64, dtype=L.F32), 1),
+    (dict(head_dim=32), 0),                       # outside the staged range (fp16/bf16)
+    (dict(head_dim=48), 0),                       # invalid problem
+])
+def test_bwd_prefers_staging(kw, want):
+    """flexatt_bwd_prefers_staging: 1 inside the staged range except fp16/bf16
+    at head_dim 64 without soft-cap or interval/block masks."""
+    assert L.load().flexatt_bwd_prefers_staging(problem(**kw)) == want
+
+
+def test_backward_staging_follows_the_preference(monkeypatch):
+    """The Python layer stages at head_dim 64 without soft-cap only when
+    ds_staging_auto is off; with soft-cap, or at head_dim 128, it stages
+    either way."""
+    import npu_flash_attention as nfa
+
+    lib = L.load()
+    plain = problem(batch=2, heads_q=8, heads_kv=2, seqlen_q=1000, seqlen_kv=1000, head_dim=64)
+    capped = problem(batch=2, heads_q=8, heads_kv=2, seqlen_q=1000, seqlen_kv=1000, head_dim=64, soft_cap=30.0)
+    d128 = problem(batch=2, heads_q=8, heads_kv=2, seqlen_q=1000, seqlen_kv=1000, head_dim=128)
+    assert nfa.ds_staging_auto is True
+    assert nfa._staged_workspace_bytes(lib, plain) == 0
+    assert nfa._staged_workspace_bytes(lib, capped) == lib.flexatt_bwd_workspace(capped) > 0
+    assert nfa._staged_workspace_bytes(lib, d128) == lib.flexatt_bwd_workspace(d128) > 0
+    monkeypatch.setattr(nfa, "ds_staging_auto", False)
+    assert nfa._staged_workspace_bytes(lib, plain) == lib.flexatt_bwd_workspace(plain) > 0
+
+
 def test_backward_selects_staging_within_the_limit(monkeypatch):
     """The Python layer's choice for one backward call: the staged backward
     with the workspace flexatt_bwd_workspace_limited gives under

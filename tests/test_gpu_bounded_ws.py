@@ -25,6 +25,12 @@ from oracle import attention_oracle as orc
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def _stage_wherever_in_range(monkeypatch):
+    # the pass plans under test, not flexatt_bwd_prefers_staging's choice
+    monkeypatch.setattr(nfa, "ds_staging_auto", False)
+
+
 def _units(sq, skv, causal, window):
     """Staged units per query head (closed form of the band)."""
     nkb = -(-skv // 128)
