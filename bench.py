@@ -240,8 +240,8 @@ def main():
     st = torch.cuda.current_stream(dev)
     sh = st.cuda_stream
     T = L.tensor
-    # the workspace the API itself sizes (npu_flash_attention.ds_workspace_limit)
-    ws_bytes = nfa._staged_workspace_bytes(lib, p)
+    # the workspace the API itself sizes (npu_flash_attention's workspace budget)
+    ws_bytes = nfa._staged_workspace_bytes(lib, p, dev)
     calls = {"fwd": lambda: lib.flexatt_fwd(p, T(q), T(k), T(v), T(o), lse.data_ptr(), sh)}
     if ws_bytes and ws_bytes < lib.flexatt_bwd_workspace(p):
         # the band exceeds the budget: the staged backward runs in passes over

@@ -73,8 +73,13 @@ ds_staging_auto = True
 # fp16/bf16, two for fp32) is used when it fits; otherwise the staged backward
 # runs in passes over chunks of whole (batch, KV-head) groups whose band fits,
 # and when not even one group fits the recomputing backward runs, whose memory
-# is O(S) like the reference's (npu_flash_attention.py:675-685).
+# is O(S) like the reference's (npu_flash_attention.py:675-685).  The budget
+# is the larger of ds_workspace_limit and ds_workspace_free_fraction of the
+# device memory free at the call (the driver's free bytes plus what torch's
+# caching allocator holds unused), so that long sequences stay on the staged
+# backward on a large-memory device; a fraction of 0 keeps the fixed limit.
 ds_workspace_limit = 4 << 30
+ds_workspace_free_fraction = 0.25
 _HEAD_DIMS = (32, 64, 128, 256)
 _BLOCK = 128  # block edge of the block-sparse map (flexatt_problem.block_map)
 
@@ -410,17 +415,36 @@ def npu_flash_attention_backward(
     return DQ, DK, DV
 
 
-def _staged_workspace_bytes(lib, p) -> int:
-    """Workspace bytes of the staged backward for problem ``p`` under
-    ``ds_workspace_limit`` (the whole band, or the band of the chunk of whole
-    (batch, KV-head) groups one pass covers); 0 selects the recomputing
-    backward (staging disabled, outside its range, slower for ``p`` under
-    ``ds_staging_auto``, or not even one group's band within the limit)."""
+def _workspace_budget(free_bytes: int) -> int:
+    """Byte budget of the staged-dS workspace given ``free_bytes`` of free
+    device memory (0: the fixed ``ds_workspace_limit`` alone)."""
+    extra = int(ds_workspace_free_fraction * max(0, int(free_bytes))) if ds_workspace_free_fraction > 0 else 0
+    return max(0, int(ds_workspace_limit), extra)
+
+
+def _free_device_bytes(device) -> int:
+    """Device memory a workspace could take now: the driver's free bytes
+    plus the bytes torch's caching allocator reserves but does not use."""
+    free, _ = torch.cuda.mem_get_info(device)
+    return int(free) + int(torch.cuda.memory_reserved(device)) - int(torch.cuda.memory_allocated(device))
+
+
+def _staged_workspace_bytes(lib, p, device=None) -> int:
+    """Workspace bytes of the staged backward for problem ``p`` under the
+    workspace budget (``ds_workspace_limit``, or ``ds_workspace_free_fraction``
+    of the free memory of ``device`` when that is larger; the whole band, or
+    the band of the chunk of whole (batch, KV-head) groups one pass covers);
+    0 selects the recomputing backward (staging disabled, outside its range,
+    slower for ``p`` under ``ds_staging_auto``, or not even one group's band
+    within the budget)."""
     if not ds_staging_enabled:
         return 0
     if ds_staging_auto and not lib.flexatt_bwd_prefers_staging(p):
         return 0
-    return int(lib.flexatt_bwd_workspace_limited(p, max(0, int(ds_workspace_limit))))
+    free = 0
+    if device is not None and ds_workspace_free_fraction > 0 and lib.flexatt_bwd_workspace(p) > ds_workspace_limit:
+        free = _free_device_bytes(device)  # queried only when the fixed limit does not hold the whole band
+    return int(lib.flexatt_bwd_workspace_limited(p, _workspace_budget(free)))
 
 
 def _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, *, causal, sliding_window,
@@ -440,7 +464,7 @@ def _backward_into(query, key, value, out, lse, grad_out, DQ, DK, DV, *, causal,
     lse = lse.to(torch.float32).contiguous()
     slopes = _alibi(alibi, Hq, query.device)
     p = _problem(q, k, scale, causal, sliding_window, soft_cap, slopes, masks)
-    ws_bytes = _staged_workspace_bytes(lib, p)
+    ws_bytes = _staged_workspace_bytes(lib, p, query.device)
     with torch.cuda.device(query.device):
         if ws_bytes:
             # the dK/dV kernel stages its dS in a workspace from torch's

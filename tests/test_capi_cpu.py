@@ -424,6 +424,34 @@ def test_backward_staging_follows_the_preference(monkeypatch):
     assert nfa._staged_workspace_bytes(lib, plain) == lib.flexatt_bwd_workspace(plain) > 0
 
 
+def test_workspace_budget_takes_a_share_of_free_memory(monkeypatch):
+    """The staged-dS budget is the larger of ds_workspace_limit and
+    ds_workspace_free_fraction of the free device memory; without a free-memory
+    figure (or with the fraction at 0) it is the fixed limit, never negative."""
+    import npu_flash_attention as nfa
+
+    assert nfa.ds_workspace_free_fraction == 0.25
+    assert nfa._workspace_budget(0) == 4 << 30
+    assert nfa._workspace_budget(8 << 30) == 4 << 30                # a quarter of 8 GiB is below the limit
+    assert nfa._workspace_budget(100 << 30) == 25 << 30
+    assert nfa._workspace_budget(-(1 << 40)) == 4 << 30
+    monkeypatch.setattr(nfa, "ds_workspace_free_fraction", 0.0)
+    assert nfa._workspace_budget(100 << 30) == 4 << 30
+    monkeypatch.setattr(nfa, "ds_workspace_limit", -5)
+    assert nfa._workspace_budget(100 << 30) == 0
+    # a long bf16 causal problem whose groups exceed 4 GiB: staged in passes
+    # once the budget covers one group, the recomputing backward below that
+    monkeypatch.setattr(nfa, "ds_workspace_limit", 4 << 30)
+    monkeypatch.setattr(nfa, "ds_workspace_free_fraction", 0.25)
+    lib = L.load()
+    big = problem(batch=1, heads_q=32, heads_kv=8, seqlen_q=65536, seqlen_kv=65536, head_dim=128, causal=1)
+    gb = 4 * _staged_units(65536, 65536, 1, 0) * 8192
+    assert gb > 4 << 30
+    assert lib.flexatt_bwd_workspace_limited(big, nfa._workspace_budget(0)) == 0
+    n = lib.flexatt_bwd_workspace_limited(big, nfa._workspace_budget(250 << 30))
+    assert n == ((250 << 30) // 4 - L.BWD_QUEUE_BYTES) // gb * gb + L.BWD_QUEUE_BYTES and n > gb
+
+
 def test_backward_selects_staging_within_the_limit(monkeypatch):
     """The Python layer's choice for one backward call: the staged backward
     with the workspace flexatt_bwd_workspace_limited gives under

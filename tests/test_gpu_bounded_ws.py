@@ -27,8 +27,10 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(autouse=True)
 def _stage_wherever_in_range(monkeypatch):
-    # the pass plans under test, not flexatt_bwd_prefers_staging's choice
+    # the pass plans under test, not flexatt_bwd_prefers_staging's choice, and
+    # under the fixed ds_workspace_limit alone (no share of free memory)
     monkeypatch.setattr(nfa, "ds_staging_auto", False)
+    monkeypatch.setattr(nfa, "ds_workspace_free_fraction", 0.0)
 
 
 def _units(sq, skv, causal, window):
@@ -125,3 +127,29 @@ def test_bounded_workspace_passes_match_oracle(gpu_device, case):
     whole = _backward(q, k, v, do, kw, 1 << 40)
     for name, x, r in zip(("dq", "dk", "dv"), got[2:], whole[2:]):
         check(name, x, r.double(), dtype)
+
+
+def test_free_memory_share_keeps_the_whole_band(gpu_device, monkeypatch):
+    """With the fixed limit below one group's band but a share of the free
+    device memory above the whole band, the backward stages the whole band in
+    one pass (instead of the recomputing fallback) and matches the oracle."""
+    dtype, cpu, (q, k, v, do), kw, ref, _, gb = _setup("bf16_d128_recompute")
+    monkeypatch.setattr(nfa, "ds_workspace_free_fraction", 0.25)
+    lib = L.load()
+    p = nfa._problem(q, k, q.shape[-1] ** -0.5, kw.get("causal", False), kw.get("sliding_window", 0),
+                     kw.get("soft_cap", 0.0), kw.get("alibi_slope"))
+    full = lib.flexatt_bwd_workspace(p)
+    assert 0.25 * nfa._free_device_bytes(q.device) > full
+    old = nfa.ds_workspace_limit
+    nfa.ds_workspace_limit = gb - 1
+    try:
+        assert nfa._staged_workspace_bytes(lib, p) == 0           # the fixed limit alone: recompute
+        assert nfa._staged_workspace_bytes(lib, p, q.device) == full  # with the free-memory share: staged
+    finally:
+        nfa.ds_workspace_limit = old
+    got = _backward(q, k, v, do, kw, gb - 1)
+    sl = kw["alibi_slope"].cpu()
+    args = (kw.get("causal", False), kw.get("sliding_window", 0), sl, kw.get("scale"), kw.get("soft_cap", 0.0))
+    want = orc.forward(*cpu[:3], *args, **ref) + tuple(orc.backward(*cpu, *args, **ref))
+    for name, x, r in zip(("o", "lse", "dq", "dk", "dv"), got, want):
+        check(name, x, r, dtype)
