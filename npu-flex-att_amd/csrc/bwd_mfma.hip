@@ -139,11 +139,11 @@ void bwd_dq_mfma_kernel(BwdArgs a) {
       const int row = c / C::CPR, col = (c % C::CPR) * 8;
       const int n = n0 + row;
       const int nc = min(n, p.Skv - 1);
-      i32x4 xk = ld_global16(kp + (int64_t)nc * a.k.ss + col);
-      i32x4 xv = ld_global16(vp + (int64_t)nc * a.v.ss + col);
-      if (n >= p.Skv) { xk = i32x4{0, 0, 0, 0}; xv = i32x4{0, 0, 0, 0}; }
-      rk[e] = xk;
-      rv[e] = xv;
+      // rows past Skv load row Skv - 1: their P is masked to 0, so they add
+      // nothing, and nothing reads the loaded registers before lstore (a
+      // select here would wait for the prefetch at once)
+      rk[e] = ld_global16(kp + (int64_t)nc * a.k.ss + col);
+      rv[e] = ld_global16(vp + (int64_t)nc * a.v.ss + col);
     }
   };
   auto lstore = [&]() {
@@ -310,20 +310,19 @@ void bwd_dkdv_mfma_kernel(BwdArgs a) {
       const int row = c / C::CPR, col = (c % C::CPR) * 8;
       const int m = m0 + row;
       const int mc = min(m, p.Sq - 1);
-      i32x4 xq = ld_global16(qp + (int64_t)mc * a.q.ss + col);
-      i32x4 xo = ld_global16(dop + (int64_t)mc * a.dout.ss + col);
-      if (m >= p.Sq) { xq = i32x4{0, 0, 0, 0}; xo = i32x4{0, 0, 0, 0}; }
-      rq[e] = xq;
-      ro[e] = xo;
+      // rows past Sq load row Sq - 1: their LSE is +inf (P = 0), so they add
+      // nothing, and nothing reads the loaded registers before lstore (a
+      // select here would wait for the prefetch at once)
+      rq[e] = ld_global16(qp + (int64_t)mc * a.q.ss + col);
+      ro[e] = ld_global16(dop + (int64_t)mc * a.dout.ss + col);
     }
     if (tid < C::BMQ) {
       const int m = m0 + tid;
-      rl = kPosInf;
+      rl = kNegInf;  // raw LSE, converted in lstore (-inf -> +inf: P = 0)
       rd = 0.f;
       if (m < p.Sq) {
         const int64_t ri = (int64_t)(b * p.Hq + hq) * p.Sq + m;
-        const float l = a.lse[ri];
-        rl = (l == kNegInf) ? kPosInf : l * kLog2e;
+        rl = a.lse[ri];
         rd = a.delta[ri];
       }
     }
@@ -337,7 +336,7 @@ void bwd_dkdv_mfma_kernel(BwdArgs a) {
       *(i32x4*)&sO[row * C::P + col] = ro[e];
     }
     if (tid < C::BMQ) {
-      sL[tid] = rl;
+      sL[tid] = (rl == kNegInf) ? kPosInf : rl * kLog2e;  // log2 units; +inf makes P exactly 0
       sDl[tid] = rd;
     }
   };
