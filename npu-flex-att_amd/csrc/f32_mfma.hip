@@ -70,10 +70,11 @@ struct Cfg {
 // fetch() starts the copy, commit() completes it in the issuing thread,
 // settle() (before the barrier that publishes the tile) waits for it.  At
 // D = 256 a row is 1 KB, one direct-to-LDS load of the wave (lane l's 16
-// bytes at row offset 16 l), so the copy holds no registers; rows past the
-// tensor repeat its last row (their scores are masked, so the finite values
-// drop out).  Otherwise the copy passes through registers and rows past the
-// tensor read as zero.
+// bytes at row offset 16 l), so the copy holds no registers.  Otherwise the
+// copy passes through registers, which nothing reads before commit() (so
+// the loads overlap the work between the two calls).  Either way rows past
+// the tensor repeat its last row: their scores are masked, so the finite
+// values drop out.
 template <int D, int NW>
 struct Tile {
   using C = Cfg<D, NW>;
@@ -97,11 +98,8 @@ struct Tile {
         const int idx = tid + i * C::NT;
         const int r = idx / (D / 4), c = 4 * (idx % (D / 4));
         const int n = r0 + r;
-        const bool in = (C::N4 % C::NT == 0 || idx < C::N4) && n < rows;
         const int nc = n < rows ? n : rows - 1;
-        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 a = *(const f32x4*)(xp + (int64_t)nc * xs + c);
-        x[i] = in ? a : zero;
+        x[i] = *(const f32x4*)(xp + (int64_t)nc * xs + c);
       }
     }
   }
