@@ -21,6 +21,11 @@ HEAD_DIMS = (32, 64, 128, 256)
 PER_D_SOURCES = ("fwd_mfma.hip", "fwd_ws.hip", "fwd_decode.hip", "bwd_mfma.hip", "bwd_kv.hip", "bwd_q.hip", "bwd_dq_ds.hip",
                   "f32_mfma.hip")
 SINGLE_SOURCES = ("delta.hip", "capi.hip")
+# Sources whose kernels load into registers through asm that the compiler
+# does not know is in flight (load16_async): a VGPR spill could store or
+# reuse such a register before its load lands, so their kernels must build
+# without scratch.
+NO_SCRATCH_SOURCES = ("bwd_dq_ds.hip",)
 
 
 def hipcc() -> str:
@@ -53,12 +58,32 @@ def jobs() -> list:
     return out
 
 
+def scratch_kernels(remarks: str) -> list:
+    """(kernel, bytes per lane) for every kernel with scratch in -Rpass-analysis=kernel-resource-usage output."""
+    out, name = [], None
+    for line in remarks.splitlines():
+        if "Function Name:" in line:
+            name = line.split("Function Name:")[1].split()[0]
+        elif "ScratchSize [bytes/lane]:" in line:
+            n = int(line.split("ScratchSize [bytes/lane]:")[1].split()[0])
+            if n > 0:
+                out.append((name, n))
+    return out
+
+
 def _compile(job):
     src, obj, extra = job
-    cmd = [hipcc()] + common_flags() + extra + ["-c", src, "-o", obj]
+    guard = os.path.basename(src) in NO_SCRATCH_SOURCES
+    cmd = [hipcc()] + common_flags() + extra + (["-Rpass-analysis=kernel-resource-usage"] if guard else []) + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    if guard:
+        bad = scratch_kernels(r.stderr)
+        if bad:
+            os.remove(obj)
+            raise RuntimeError(f"{os.path.basename(src)} {' '.join(extra)}: kernels with asm register loads use scratch "
+                               f"(a spilled register could be reused while its load is in flight): {bad}")
     return obj
 
 

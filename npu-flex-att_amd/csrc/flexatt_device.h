@@ -136,7 +136,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 // 16 bytes global -> registers, issued through asm like load_lds16 so that
 // the compiler's wait counting does not see it; the data may be read only
 // after wait_vmcnt_tied<N>(...) names the destination registers (the tie
-// keeps every use of them after the wait).
+// keeps every use of them after the wait).  The compiler does not know the
+// load is in flight, so a kernel that uses it must keep the destination
+// registers in place: one that spills VGPRs may store such a register to
+// scratch and reuse it before the load lands (the landing load then
+// overwrites whatever the register holds by then).  build_lib.py rejects a
+// build in which a kernel of such a source uses scratch.
 __device__ __forceinline__ void load16_async(i32x4& dst, const void* gptr) {
   asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(dst) : "v"(gptr) : "memory");
 }

@@ -482,3 +482,19 @@ def test_backward_selects_staging_within_the_limit(monkeypatch):
     monkeypatch.setattr(nfa, "ds_workspace_limit", 4 << 30)
     assert lib.flexatt_bwd_workspace(big) > 130e9
     assert nfa._staged_workspace_bytes(lib, big) == 0
+
+
+def test_build_rejects_scratch_in_async_load_kernels():
+    """The build guard reads the compiler's resource remarks: any kernel of a
+    source with asm register loads that uses scratch fails the build."""
+    import build_lib
+    remarks = "\n".join([
+        "x.hip:1:1: remark: Function Name: _ZN7flexatt1aE [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark: Function Name: _ZN7flexatt1bE [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     VGPRs: 128 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     ScratchSize [bytes/lane]: 92 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert build_lib.scratch_kernels(remarks) == [("_ZN7flexatt1bE", 92)]
+    assert build_lib.scratch_kernels("") == []
+    assert "bwd_dq_ds.hip" in build_lib.NO_SCRATCH_SOURCES
