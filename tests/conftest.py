@@ -26,8 +26,8 @@ def gpu_device():
 
 def pytest_sessionfinish(session, exitstatus):
     """Write the parity errors the GPU tests measured (gpu_helpers.RECORDS)
-    as JSON lines to $FLEXATT_PARITY_LOG, or gpurun_out/parity_errors.jsonl
-    when that folder exists."""
+    as JSON lines to $FLEXATT_PARITY_LOG, or to parity_errors.jsonl in the
+    repository's GPU-run output folder when that folder exists."""
     mod = sys.modules.get("gpu_helpers")
     recs = getattr(mod, "RECORDS", None)
     if not recs:

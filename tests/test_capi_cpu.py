@@ -180,8 +180,8 @@ def _integration_stub():
 
 
 def test_integration_stub_matches_the_abi(monkeypatch):
-    """The reference-side binding documented in INTEGRATION.md runs against
-    the built library (it checks the ABI version itself) and its structs have
+    """The reference-side ctypes binding given in the integration guide runs
+    against the built library (it checks the ABI version itself) and its structs have
     the header's size and field offsets."""
     monkeypatch.setenv("FLEXATT_LIB", L.LIB_PATH)
     L.load()
