@@ -296,13 +296,16 @@ __device__ __forceinline__ void kv_tile_stream(const BwdArgs& a, char* smem, int
             wk(kk, w, k);
             return lds_read16(smem + (ra[w][k >> 1] + (k & 1) * C::TILEB));
           };
-          i32x4 ab[5];
+          // Q / dO rows read SAK MFMAs ahead (six: 0.5% faster than four over
+          // the 64 MFMAs of a two-tile step; eight is slower)
+          constexpr int SAK = 6;
+          i32x4 ab[SAK + 1];
 #pragma unroll
-          for (int kk = 0; kk < 4; ++kk) ab[kk] = rdA(kk);
+          for (int kk = 0; kk < SAK; ++kk) ab[kk] = rdA(kk);
 #pragma unroll
           for (int kk = 0; kk < NT; ++kk) {
             __builtin_amdgcn_sched_barrier(0);
-            if (kk + 4 < NT) ab[(kk + 4) % 5] = rdA(kk + 4);
+            if (kk + SAK < NT) ab[(kk + SAK) % (SAK + 1)] = rdA(kk + SAK);
             int w, k;
             wk(kk, w, k);
             if (k == LREAD) {
@@ -313,8 +316,8 @@ __device__ __forceinline__ void kv_tile_stream(const BwdArgs& a, char* smem, int
 #pragma unroll
               for (int jj = 0; jj < 4; ++jj) L4[w][k - LCONV][jj] *= kLog2e;
             }
-            if (k & 1) DP[w] = M::mma(as_v8<V8>(ab[kk % 5]), vreg[k >> 1], DP[w]);
-            else S[w] = M::mma(as_v8<V8>(ab[kk % 5]), kreg[k >> 1], S[w]);
+            if (k & 1) DP[w] = M::mma(as_v8<V8>(ab[kk % (SAK + 1)]), vreg[k >> 1], DP[w]);
+            else S[w] = M::mma(as_v8<V8>(ab[kk % (SAK + 1)]), kreg[k >> 1], S[w]);
           }
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
